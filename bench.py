@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A8 linear-layer path (one GPU).
+
+Headline (`value`): BASELINE configs[1] -- decode GEMV, M=1 token, g256, the
+four linears of a Qwen3-4B-class DualAR layer (qkv K=2560 N=6144, o K=4096
+N=2560, gate_up K=2560 N=19456, down K=9728 N=2560), each through the drop-in
+entry point fa_w8a8_gemm (dynamic per-(token, group) activation quant + int8
+GEMV + fp32 dequant-sum + fp16 out).  One step = those four linears for each
+of 36 layers with distinct weights (3.6 GB), so weights stream from HBM and
+not from the 256 MB last-level cache; the step is replayed from a HIP graph.
+value = algorithmic bytes (int8 W + fp16 scales + fp16 x + fp16 y) / time.
+
+Extra objects on the same JSON line: roofline of the dominant kernel (the
+gate_up GEMV, timed with HIP events on its own stream), the CPU baseline (the
+scalar C oracle with OpenMP on this host), and secondary figures for configs
+[2] (M=8 g64), [3] (prefill M=512/2048 int8 TOPS) and [4] (36-layer decode
+stack with fused prologues).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "fish-audio-cpp_amd"))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "decode GEMV HBM GB/s + prefill INT8 TOPS (% of MI355X peak), g256/g64"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, reps, torch):
+    """Average duration of fn() measured with events on the current stream."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(reps):
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    return times
+
+
+def cpu_baseline(stack, torch, budget_s):
+    """configs[1] on the host: the C oracle (scalar C restatement of the
+    reference's W8A8 math, OpenMP over output rows) for one layer's four
+    linears at M=1 g256; median over repetitions within budget_s."""
+    from oracle import ref
+    from fish_amd.synth import LAYER_SHAPES
+    lay = stack.layers[0]
+    host = {}
+    nbytes = 0
+    for name, (K, N) in LAYER_SHAPES.items():
+        L = lay[name]
+        host[name] = (L.W.cpu().numpy(), L.scale.cpu().numpy(),
+                      stack.x_in[name].cpu().numpy())
+        nbytes += L.algo_bytes + 2 * (K + N)
+    threads = ref.num_threads()
+
+    def one():
+        for name, (W, S, X) in host.items():
+            ref.w8a8_gemm(W, S, stack.g, X)
+
+    one()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": "one layer's 4 linears (qkv/o/gate_up/down) at M=1 g256, "
+                      "%d reps, median %.2f ms" % (len(times), med * 1e3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the gate_up GEMV event timing (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from fish_amd import ops
+    from fish_amd.decode_stack import DecodeStack
+    from fish_amd.synth import LAYER_SHAPES
+
+    torch.cuda.init()
+    log("building 36-layer g256 weight set ...")
+    st = DecodeStack(n_layers=args.layers, g=256, tokens=1, seed=0)
+    torch.cuda.synchronize()
+
+    if args.roofline_only:
+        r = roofline_gate_up(torch, ops, st, LAYER_SHAPES)
+        print(json.dumps({"roofline": r}), flush=True)
+        return
+
+    # ---- headline: configs[1] linears, graph-replayed --------------------
+    graph = st.capture(lambda: st.run_linears())
+    eager_y = {k: v.clone() for k, v in st.y.items()}
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    for k in st.y:   # graph replays reproduce the eager result
+        assert torch.equal(st.y[k], eager_y[k]), k
+    ms_per_step = dt / args.steps * 1e3
+    step_bytes = st.linears_bytes()
+    value = step_bytes / (dt / args.steps) / 1e9
+
+    roofline = roofline_gate_up(torch, ops, st, LAYER_SHAPES)
+
+    secondary = {}
+    if not args.no_secondary:
+        secondary = run_secondary(torch, ops, st, args)
+
+    cpu = cpu_baseline(st, torch, args.cpu_budget)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: decode M=1 g256, qkv/o/gate_up/down via "
+                               "fa_w8a8_gemm (quant + GEMV), 36 layers of distinct weights "
+                               "per step, HIP-graph replay",
+                   "tokens": 1, "group_size": 256, "layers_per_step": args.layers,
+                   "bytes_per_step": step_bytes, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def roofline_gate_up(torch, ops, st, LAYER_SHAPES):
+    # ---- roofline: dominant kernel (gate_up GEMV) timed with HIP events ---
+    # x is quantized once; the events bracket only the GEMV launches, on the
+    # stream they are launched on (torch's current stream).
+    L0 = st.layers[0]["gate_up"]
+    xq, xs = ops.quantize_activations(st.x_in["gate_up"], 256)
+    out = st.y["gate_up"]
+
+    def gemv_all_layers():
+        for lay in st.layers:
+            L = lay["gate_up"]
+            ops.w8a8_gemm_quantized(L.W, L.scale, 256, xq, xs, out=out)
+
+    gemv_all_layers()
+    torch.cuda.synchronize()
+    # Pre-load the stream with ~1 ms of unrelated work so the host has queued
+    # every (event, kernel, event) triple before the GPU reaches them: the
+    # events then bracket back-to-back kernels, not host launch latency.
+    pre = torch.randn((8192, 8192), device="cuda").half()
+    per_launch = []
+    s_ev = [torch.cuda.Event(enable_timing=True) for _ in st.layers]
+    e_ev = [torch.cuda.Event(enable_timing=True) for _ in st.layers]
+    for _ in range(3):
+        torch.mm(pre, pre)
+        for i, lay in enumerate(st.layers):
+            L = lay["gate_up"]
+            s_ev[i].record()
+            ops.w8a8_gemm_quantized(L.W, L.scale, 256, xq, xs, out=out)
+            e_ev[i].record()
+        torch.cuda.synchronize()
+        per_launch += [s_ev[i].elapsed_time(e_ev[i]) for i in range(len(st.layers))]
+    del pre
+    avg_ms = statistics.mean(per_launch)
+    K, N = LAYER_SHAPES["gate_up"]
+    kbytes = L0.algo_bytes + 2 * (K + N)
+    achieved = kbytes / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_mfma_kernel (gate_up, K=2560 N=19456, M=1, g256)",
+                "avg_launch_us": round(avg_ms * 1e3, 3), "bytes_per_launch": kbytes}
+
+
+
+def run_secondary(torch, ops, st, args):
+    from fish_amd.decode_stack import DecodeStack
+    from fish_amd.synth import LAYER_SHAPES
+    out = {}
+    # full decode-step linear stack with fused prologues (g256)
+    st.h.copy_(st.h0)
+    g_stack = st.capture(lambda: st.run_stack())
+    for _ in range(2):
+        g_stack.replay()
+    torch.cuda.synchronize()
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_stack.replay()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    out["cfg4_stack_g256_m1"] = {"step_ms": round(t * 1e3, 4),
+                                 "GB/s": round(st.stack_bytes() / t / 1e9, 1)}
+    # configs[1] per-linear GEMV time (events, eager, weights cold over layers)
+    for name, (K, N) in LAYER_SHAPES.items():
+        xq, xs = ops.quantize_activations(st.x_in[name], 256)
+        y = st.y[name]
+
+        def run(name=name, xq=xq, xs=xs, y=y):
+            for lay in st.layers:
+                L = lay[name]
+                ops.w8a8_gemm_quantized(L.W, L.scale, 256, xq, xs, out=y)
+        run()
+        ms = statistics.median(event_time_ms(run, 3, torch)) / len(st.layers)
+        b = st.layers[0][name].algo_bytes + 2 * (K + N)
+        out["cfg1_gemv_%s_us" % name] = round(ms * 1e3, 2)
+        out["cfg1_gemv_%s_GBs" % name] = round(b / (ms * 1e-3) / 1e9, 1)
+    del st
+    torch.cuda.empty_cache()
+
+    # M=8, g64 (smaller layer count keeps the bench short)
+    st8 = DecodeStack(n_layers=12, g=64, tokens=8, seed=1)
+    for name, (K, N) in LAYER_SHAPES.items():
+        xq, xs = ops.quantize_activations(st8.x_in[name], 64)
+        y = st8.y[name]
+
+        def run8(name=name, xq=xq, xs=xs, y=y):
+            for lay in st8.layers:
+                L = lay[name]
+                ops.w8a8_gemm_quantized(L.W, L.scale, 64, xq, xs, out=y)
+        run8()
+        ms = statistics.median(event_time_ms(run8, 3, torch)) / len(st8.layers)
+        b = st8.layers[0][name].algo_bytes + 2 * 8 * (K + N)
+        out["cfg2_gemv_m8_g64_%s_GBs" % name] = round(b / (ms * 1e-3) / 1e9, 1)
+    del st8
+    torch.cuda.empty_cache()
+
+    # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    for g in (256, 64):
+        for M in ((512, 2048) if g == 256 else (2048,)):
+            tot_ops, tot_ms = 0.0, 0.0
+            for name, (K, N) in LAYER_SHAPES.items():
+                w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+                W, S = ops.quantize_weights_groupwise(w, g)
+                del w
+                x = torch.randn((M, K), generator=gen, device="cuda").half()
+                xq, xs = ops.quantize_activations(x, g)
+                y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+                f = lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=y)
+                f()
+                ms = statistics.median(event_time_ms(f, 5, torch))
+                o = 2.0 * M * N * K
+                tot_ops += o
+                tot_ms += ms
+                out["cfg3_gemm_m%d_g%d_%s_TOPS" % (M, g, name)] = round(o / (ms * 1e-3) / 1e12, 1)
+            tops = tot_ops / (tot_ms * 1e-3) / 1e12
+            out["cfg3_gemm_m%d_g%d_layer_TOPS" % (M, g)] = round(tops, 1)
+            out["cfg3_gemm_m%d_g%d_frac_int8_peak" % (M, g)] = round(tops / INT8_PEAK_TOPS, 4)
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,369 @@
+// api.cpp -- the C ABI (include/fish_w8a8.h): argument checks, scratch
+// management and kernel dispatch.
+//
+// Dispatch for the linear layer (reference dispatcher: int8_gemm.cu:384-511):
+//   K % 64 == 0, group % 64 == 0, 16-byte aligned W and X_q:
+//       N <= 16  -> decode GEMV on int8 MFMA (gemv.hip), split over K-groups
+//       N  > 16  -> LDS-tiled int8 MFMA GEMM (gemm.hip)
+//   anything else -> the exact any-shape kernel (gemm.hip, generic)
+// The error convention mirrors CUDA_CHECK (src/utils/cuda_utils.h:10-17): a
+// failing HIP call is reported with file/line and hipGetErrorString, here as
+// a status code plus a per-thread message instead of an exception.
+#include "common.h"
+#include "../../include/fish_w8a8.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <unordered_map>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define FA_HIP(call)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(FA_ERR_HIP, "HIP error at %s:%d: %s", __FILE__, __LINE__,      \
+                        hipGetErrorString(e_));                                        \
+    } while (0)
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Per-thread, per-device grow-only scratch (the reference keeps a thread_local
+// workspace, int8_gemm.cu:31-44).
+struct Workspace {
+    int8_t* xq = nullptr;
+    size_t xq_bytes = 0;
+    float* xs = nullptr;
+    size_t xs_bytes = 0;
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    int* counters = nullptr;
+    size_t counter_count = 0;
+};
+
+thread_local std::unordered_map<int, Workspace> g_ws;
+
+int current_ws(Workspace** out) {
+    int dev = 0;
+    FA_HIP(hipGetDevice(&dev));
+    *out = &g_ws[dev];
+    return FA_OK;
+}
+
+int grow(void** p, size_t* have, size_t need, hipStream_t stream) {
+    if (*have >= need) return FA_OK;
+    need = (need + 255) & ~(size_t)255;
+    if (*p) {
+        FA_HIP(hipStreamSynchronize(stream));
+        FA_HIP(hipFree(*p));
+        *p = nullptr;
+        *have = 0;
+    }
+    FA_HIP(hipMalloc(p, need));
+    *have = need;
+    return FA_OK;
+}
+
+int grow_counters(Workspace& ws, size_t count, hipStream_t stream) {
+    if (ws.counter_count >= count) return FA_OK;
+    size_t bytes_have = ws.counter_count * sizeof(int);
+    void* p = ws.counters;
+    int rc = grow(&p, &bytes_have, count * sizeof(int), stream);
+    if (rc) return rc;
+    ws.counters = (int*)p;
+    ws.counter_count = bytes_have / sizeof(int);
+    // Counters start at zero; the GEMV re-arms each one after use.
+    FA_HIP(hipMemset(ws.counters, 0, bytes_have));
+    return FA_OK;
+}
+
+int eff_group(int K, int g) { return (g <= 0 || g > K) ? K : g; }
+
+bool fast_shape(const int8_t* W, const int8_t* xq, int K, int g) {
+    return (K % 64 == 0) && (g % 64 == 0) && aligned16(W) && aligned16(xq);
+}
+
+// Worst-case split-K scratch (floats) of the GEMV for N tokens and M rows.
+size_t gemv_part_floats(int M, int N, int K, int g, int G) {
+    fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
+    return p.splits > 1 ? (size_t)p.splits * (size_t)N * (size_t)M : 0;
+}
+
+int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, int g, int G,
+                     const int8_t* xq, const float* xs, uint16_t* Y, int32_t* dbg, int row0,
+                     int rows, int tok0, int toks, int M, int N, int K, hipStream_t stream) {
+    if (fast_shape(W, xq, K, g)) {
+        if (N <= 16) {
+            fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
+            Workspace* ws = nullptr;
+            int rc = current_ws(&ws);
+            if (rc) return rc;
+            if (p.splits > 1) {
+                void* part = ws->part;
+                rc = grow(&part, &ws->part_bytes,
+                          (size_t)p.splits * (size_t)N * (size_t)M * sizeof(float), stream);
+                ws->part = (float*)part;
+                if (rc) return rc;
+                rc = grow_counters(*ws, (size_t)p.tiles, stream);
+                if (rc) return rc;
+            }
+            FA_HIP(fa::launch_gemv(p, W, w_scale, xq, xs, Y, ws->part, ws->counters, dbg, row0,
+                                   rows, tok0, toks, M, N, K, g, G, stream));
+            return FA_OK;
+        }
+        FA_HIP(fa::launch_gemm(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g, G,
+                               stream));
+        return FA_OK;
+    }
+    if (N > 65535) return fail(FA_ERR_INVALID_ARG, "%s: N=%d too large for the generic path", fn, N);
+    FA_HIP(fa::launch_gemm_generic(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g,
+                                   G, stream));
+    return FA_OK;
+}
+
+int check_dims(const char* fn, int M, int N, int K) {
+    if (M < 0 || N < 0) return fail(FA_ERR_INVALID_ARG, "%s: negative M=%d or N=%d", fn, M, N);
+    if (K <= 0) return fail(FA_ERR_INVALID_ARG, "%s: K=%d must be positive", fn, K);
+    return FA_OK;
+}
+
+}  // namespace
+
+namespace fa {
+void set_last_error(const std::string& msg) { g_err = msg; }
+}  // namespace fa
+
+extern "C" {
+
+const char* fa_last_error(void) { return g_err.c_str(); }
+
+const char* fa_version(void) { return "fish-w8a8-mi355x 0.1.0 (gfx950)"; }
+
+int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_size,
+                           const int8_t* X_q, const float* X_scale, uint16_t* Y, int M, int N,
+                           int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_quantized";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !X_q || !X_scale || !Y)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    return linear_quantized(fn, W, w_scale, g, G, X_q, X_scale, Y, nullptr, 0, 0, 0, 0, M, N, K,
+                            (hipStream_t)stream);
+}
+
+int fa_w8a8_gemm_partials(const int8_t* W, const uint16_t* w_scale, int group_size,
+                          const int8_t* X_q, const float* X_scale, uint16_t* Y, int32_t* partials,
+                          int row0, int rows, int tok0, int toks, int M, int N, int K,
+                          void* stream) {
+    const char* fn = "fa_w8a8_gemm_partials";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !X_q || !X_scale || !Y || !partials)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (row0 < 0 || rows <= 0 || row0 + rows > M || tok0 < 0 || toks <= 0 || tok0 + toks > N)
+        return fail(FA_ERR_INVALID_ARG, "%s: window rows [%d,+%d) toks [%d,+%d) outside M=%d N=%d",
+                    fn, row0, rows, tok0, toks, M, N);
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    return linear_quantized(fn, W, w_scale, g, G, X_q, X_scale, Y, partials, row0, rows, tok0,
+                            toks, M, N, K, (hipStream_t)stream);
+}
+
+int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
+                 const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* X,
+                 uint16_t* Y, int M, int N, int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !X || !Y) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    hipStream_t s = (hipStream_t)stream;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    Workspace* ws = nullptr;
+    rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->xq;
+    rc = grow(&p, &ws->xq_bytes, (size_t)N * (size_t)K, s);
+    ws->xq = (int8_t*)p;
+    if (rc) return rc;
+    p = ws->xs;
+    rc = grow(&p, &ws->xs_bytes, (size_t)N * (size_t)G * sizeof(float), s);
+    ws->xs = (float*)p;
+    if (rc) return rc;
+    FA_HIP(fa::launch_quantize_activations(X, nullptr, fa::Prologue::kPlain, act_scale, smooth_inv,
+                                           ws->xq, ws->xs, nullptr, N, K, g, G, s));
+    return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
+                            s);
+}
+
+int fa_quantize_activations(const uint16_t* X, const uint16_t* act_scale,
+                            const uint16_t* smooth_inv, int8_t* X_q, float* X_scale, int N, int K,
+                            int group_size, void* stream) {
+    const char* fn = "fa_quantize_activations";
+    g_err.clear();
+    int rc = check_dims(fn, 0, N, K);
+    if (rc) return rc;
+    if (N == 0) return FA_OK;
+    if (!X || !X_q || !X_scale) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    FA_HIP(fa::launch_quantize_activations(X, nullptr, fa::Prologue::kPlain, act_scale, smooth_inv,
+                                           X_q, X_scale, nullptr, N, K, g, G,
+                                           (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_rms_norm(const uint16_t* x, const uint16_t* weight, uint16_t* out, int n_tokens, int dim,
+                float eps, void* stream) {
+    const char* fn = "fa_rms_norm";
+    g_err.clear();
+    if (n_tokens < 0 || dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad n_tokens=%d dim=%d", fn, n_tokens, dim);
+    if (n_tokens == 0) return FA_OK;
+    if (!x || !weight || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
+    FA_HIP(fa::launch_rms_norm_quant(x, weight, eps, nullptr, nullptr, dim, 1, nullptr, nullptr,
+                                     out, n_tokens, dim, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
+                      const uint16_t* smooth_inv, const uint16_t* act_scale, int group_size,
+                      int8_t* X_q, float* X_scale, uint16_t* out, int n_tokens, int dim,
+                      void* stream) {
+    const char* fn = "fa_rms_norm_quant";
+    g_err.clear();
+    if (n_tokens < 0 || dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad n_tokens=%d dim=%d", fn, n_tokens, dim);
+    if (n_tokens == 0) return FA_OK;
+    if (!x || !weight || !X_q || !X_scale)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
+    const int g = eff_group(dim, group_size);
+    const int G = (dim + g - 1) / g;
+    FA_HIP(fa::launch_rms_norm_quant(x, weight, eps, smooth_inv, act_scale, g, G, X_q, X_scale, out,
+                                     n_tokens, dim, (hipStream_t)stream));
+    return FA_OK;
+}
+
+static int elementwise(const char* fn, int op, uint16_t* a, const uint16_t* b, int64_t n,
+                       void* stream) {
+    g_err.clear();
+    if (n < 0) return fail(FA_ERR_INVALID_ARG, "%s: negative n", fn);
+    if (n == 0) return FA_OK;
+    if (!a || (op != 0 && !b)) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    FA_HIP(fa::launch_elementwise(op, a, b, n, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_silu(uint16_t* x, int64_t n, void* stream) {
+    return elementwise("fa_silu", 0, x, nullptr, n, stream);
+}
+int fa_mul(uint16_t* a, const uint16_t* b, int64_t n, void* stream) {
+    return elementwise("fa_mul", 1, a, b, n, stream);
+}
+int fa_residual_add(uint16_t* a, const uint16_t* b, int64_t n, void* stream) {
+    return elementwise("fa_residual_add", 2, a, b, n, stream);
+}
+
+int fa_silu_mul_quant(const uint16_t* gate, const uint16_t* up, const uint16_t* smooth_inv,
+                      const uint16_t* act_scale, int group_size, int8_t* X_q, float* X_scale,
+                      uint16_t* out, int n_tokens, int dim, void* stream) {
+    const char* fn = "fa_silu_mul_quant";
+    g_err.clear();
+    if (n_tokens < 0 || dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad n_tokens=%d dim=%d", fn, n_tokens, dim);
+    if (n_tokens == 0) return FA_OK;
+    if (!gate || !up || !X_q || !X_scale)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    const int g = eff_group(dim, group_size);
+    const int G = (dim + g - 1) / g;
+    FA_HIP(fa::launch_quantize_activations(gate, up, fa::Prologue::kSiluMul, act_scale, smooth_inv,
+                                           X_q, X_scale, out, n_tokens, dim, g, G,
+                                           (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, int group_size,
+                                  int8_t* q, uint16_t* scale, void* stream) {
+    const char* fn = "fa_quantize_weights_groupwise";
+    g_err.clear();
+    if (rows < 0 || K <= 0 || group_size <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad rows=%lld K=%lld group_size=%d", fn,
+                    (long long)rows, (long long)K, group_size);
+    if (rows == 0) return FA_OK;
+    if (!w || !q || !scale) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    FA_HIP(fa::launch_quantize_weights(w, rows, K, group_size, q, scale, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_size, void* stream) {
+    const char* fn = "fa_workspace_reserve";
+    g_err.clear();
+    if (max_tokens < 0 || max_M < 0 || max_K <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad sizes", fn);
+    hipStream_t s = (hipStream_t)stream;
+    const int g = eff_group(max_K, min_group_size);
+    const int G = (max_K + g - 1) / g;
+    Workspace* ws = nullptr;
+    int rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->xq;
+    rc = grow(&p, &ws->xq_bytes, (size_t)max_tokens * (size_t)max_K, s);
+    ws->xq = (int8_t*)p;
+    if (rc) return rc;
+    p = ws->xs;
+    rc = grow(&p, &ws->xs_bytes, (size_t)max_tokens * (size_t)G * sizeof(float), s);
+    ws->xs = (float*)p;
+    if (rc) return rc;
+    // GEMV split scratch: splits * M is at most (2560 + tiles) * 16 for any M.
+    const int n16 = max_tokens < 16 ? max_tokens : 16;
+    size_t worst = 0;
+    for (int m = 16; m <= max_M + 15; m += 16) {
+        size_t f = gemv_part_floats(m, n16, max_K, g, G);
+        if (f > worst) worst = f;
+        if (m > 65536) break;
+    }
+    p = ws->part;
+    rc = grow(&p, &ws->part_bytes, worst * sizeof(float), s);
+    ws->part = (float*)p;
+    if (rc) return rc;
+    return grow_counters(*ws, (size_t)fa::ceil_div(max_M > 0 ? max_M : 1, 16), s);
+}
+
+int fa_workspace_release(void) {
+    g_err.clear();
+    Workspace* ws = nullptr;
+    int rc = current_ws(&ws);
+    if (rc) return rc;
+    FA_HIP(hipDeviceSynchronize());
+    if (ws->xq) FA_HIP(hipFree(ws->xq));
+    if (ws->xs) FA_HIP(hipFree(ws->xs));
+    if (ws->part) FA_HIP(hipFree(ws->part));
+    if (ws->counters) FA_HIP(hipFree(ws->counters));
+    *ws = Workspace{};
+    return FA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// common.h -- shared device helpers and launcher declarations for the W8A8 path.
+//
+// Conventions (kept from the reference kernel API, src/kernels/kernels.h:242-259):
+//   M = output features (rows of the int8 weight W [M, K], row-major),
+//   N = tokens (X [N, K] row-major fp16), Y is col-major [M, N] = row-major
+//   [N tokens, M].  Weight scales are fp16 [M] (one group) or [M, G] row-major.
+//   Activation scales are fp32 [N, G] row-major, X_q int8 [N, K] row-major.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace fa {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+// Round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
+// The empty asm pins `f` as an fp32 register value: without it the backend
+// folds `f2h(a * b)` into v_fma_mixlo_f16, which rounds the product once,
+// straight to fp16, instead of to fp32 and then to fp16 as the reference's
+// `__float2half(a * b)` does.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
+    return __half_as_ushort(__float2half(f));
+}
+
+// Activation quantization of one value given 1/scale, as the reference
+// quantizer does it (src/kernels/int8_gemm.cu:202-209): RN-even, clamp +-127.
+__device__ __forceinline__ int quant_rn(float v, float inv) {
+    float t = __builtin_rintf(v * inv);
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    return (int)t;
+}
+
+// Dynamic scale from a group max (int8_gemm.cu:197-198) or a static scale
+// (:185-186): both clamped below at 1e-8.
+__device__ __forceinline__ float act_scale_from_amax(float amax) {
+    float s = amax / 127.0f;
+    return s < 1e-8f ? 1e-8f : s;
+}
+
+// Wave64 max/sum over lane subgroups of width W (a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float subgroup_max(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace fa
+
+// ---------------------------------------------------------------------------
+// Launchers (host functions, one per kernel family).  They validate nothing:
+// the C-ABI layer (api.cpp) checks shapes and alignment before calling them.
+// Each returns the hipError_t of the launch.
+// ---------------------------------------------------------------------------
+namespace fa {
+
+// Prologue kinds for the activation quantizer.
+enum class Prologue : int { kPlain = 0, kSiluMul = 1 };
+
+hipError_t launch_quantize_activations(const uint16_t* X, const uint16_t* up, Prologue kind,
+                                       const uint16_t* act_scale, const uint16_t* smooth_inv,
+                                       int8_t* x_q, float* x_scale, uint16_t* out_f16,
+                                       int N, int K, int g, int G, hipStream_t stream);
+
+hipError_t launch_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
+                                 const uint16_t* smooth_inv, const uint16_t* act_scale,
+                                 int g, int G, int8_t* x_q, float* x_scale, uint16_t* out_f16,
+                                 int n_tokens, int dim, hipStream_t stream);
+
+hipError_t launch_elementwise(int op, uint16_t* a, const uint16_t* b, int64_t n,
+                              hipStream_t stream);
+
+hipError_t launch_quantize_weights(const uint16_t* w, int64_t rows, int64_t K, int g,
+                                   int8_t* q, uint16_t* scale, hipStream_t stream);
+
+// Decode GEMV (N <= 16 tokens) on int8 MFMA.  part/counters: split-K scratch.
+struct GemvPlan {
+    int tiles;   // ceil(M / 16)
+    int splits;  // K-group splits across workgroups
+    int gps;     // groups per split
+};
+GemvPlan plan_gemv(int M, int N, int K, int g, int G);
+// Debug window: when dbg_partials is non-null the kernels also write the exact
+// int32 partial of every (token, row, group) inside
+// [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to
+// dbg_partials[((tok - dbg_tok0) * dbg_rows + (row - dbg_row0)) * G + group].
+hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
+                       const int8_t* x_q, const float* x_scale, uint16_t* Y, float* part,
+                       int* counters, int32_t* dbg_partials, int dbg_row0, int dbg_rows,
+                       int dbg_tok0, int dbg_toks, int M, int N, int K, int g, int G,
+                       hipStream_t stream);
+
+// Prefill GEMM on int8 MFMA with LDS-staged tiles.
+hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                       const float* x_scale, uint16_t* Y, int32_t* dbg_partials, int dbg_row0,
+                       int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g, int G,
+                       hipStream_t stream);
+
+// Any-shape fallback (any K, any group size, unaligned pointers).
+hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                               const float* x_scale, uint16_t* Y, int32_t* dbg_partials,
+                               int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M,
+                               int N, int K, int g, int G, hipStream_t stream);
+
+}  // namespace fa

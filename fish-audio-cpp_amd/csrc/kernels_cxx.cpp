@@ -1,0 +1,62 @@
+// kernels_cxx.cpp -- fish::kernels C++ entry points over the C ABI; a failure
+// throws std::runtime_error with fa_last_error(), as the reference's
+// CUDA_CHECK does (src/utils/cuda_utils.h:10-17).
+#include "fish_amd/kernels.h"
+#include "../../include/fish_w8a8.h"
+
+#include <stdexcept>
+#include <string>
+
+namespace fish::kernels {
+namespace {
+inline const uint16_t* u16(const __half* p) { return reinterpret_cast<const uint16_t*>(p); }
+inline uint16_t* u16(__half* p) { return reinterpret_cast<uint16_t*>(p); }
+inline void check(int rc) {
+    if (rc != FA_OK) throw std::runtime_error(std::string("fish::kernels: ") + fa_last_error());
+}
+}  // namespace
+
+void rms_norm(const __half* x, const __half* weight, __half* out, int n_tokens, int dim, float eps,
+              hipStream_t stream) {
+    check(fa_rms_norm(u16(x), u16(weight), u16(out), n_tokens, dim, eps, stream));
+}
+
+void silu_forward(__half* x, int n, hipStream_t stream) { check(fa_silu(u16(x), n, stream)); }
+
+void mul_forward(__half* a, const __half* b, int n, hipStream_t stream) {
+    check(fa_mul(u16(a), u16(b), n, stream));
+}
+
+void residual_add(__half* a, const __half* b, int n, hipStream_t stream) {
+    check(fa_residual_add(u16(a), u16(b), n, stream));
+}
+
+void int8_dequant_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                            const __half* act_scale, const __half* smooth_inv, const __half* X,
+                            __half* Y, int M, int N, int K, void* /*blas_handle_unused*/,
+                            hipStream_t stream) {
+    check(fa_w8a8_gemm(W, u16(scale), group_size, u16(act_scale), u16(smooth_inv), u16(X), u16(Y),
+                       M, N, K, stream));
+}
+
+void rms_norm_quant(const __half* x, const __half* weight, float eps, const __half* smooth_inv,
+                    const __half* act_scale, int group_size, int8_t* X_q, float* X_scale,
+                    __half* out, int n_tokens, int dim, hipStream_t stream) {
+    check(fa_rms_norm_quant(u16(x), u16(weight), eps, u16(smooth_inv), u16(act_scale), group_size,
+                            X_q, X_scale, u16(out), n_tokens, dim, stream));
+}
+
+void silu_mul_quant(const __half* gate, const __half* up, const __half* smooth_inv,
+                    const __half* act_scale, int group_size, int8_t* X_q, float* X_scale,
+                    __half* out, int n_tokens, int dim, hipStream_t stream) {
+    check(fa_silu_mul_quant(u16(gate), u16(up), u16(smooth_inv), u16(act_scale), group_size, X_q,
+                            X_scale, u16(out), n_tokens, dim, stream));
+}
+
+void int8_gemm_quantized_fp16(const int8_t* W, const __half* scale, int group_size,
+                              const int8_t* X_q, const float* X_scale, __half* Y, int M, int N,
+                              int K, hipStream_t stream) {
+    check(fa_w8a8_gemm_quantized(W, u16(scale), group_size, X_q, X_scale, u16(Y), M, N, K, stream));
+}
+
+}  // namespace fish::kernels

@@ -1,0 +1,102 @@
+"""ctypes binding of libfish_w8a8.so (the C ABI in include/fish_w8a8.h).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for any entry point.
+"""
+import ctypes
+import os
+
+from .build import LIB_PATH
+
+FA_OK = 0
+FA_ERR_INVALID_ARG = 1
+FA_ERR_HIP = 2
+FA_ERR_IO = 3
+FA_ERR_FORMAT = 4
+FA_ERR_NOT_FOUND = 5
+
+_c = ctypes
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+
+
+class TensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("dtype", ctypes.c_uint32),
+        ("ndim", ctypes.c_uint32),
+        ("shape", ctypes.c_int64 * 8),
+        ("offset", ctypes.c_uint64),
+        ("size", ctypes.c_uint64),
+        ("data", ctypes.c_void_p),
+    ]
+
+
+class QuantMeta(ctypes.Structure):
+    _fields_ = [
+        ("has_scale", ctypes.c_int),
+        ("has_smooth_inv", ctypes.c_int),
+        ("has_act_scale", ctypes.c_int),
+        ("group_size", ctypes.c_int),
+        ("M", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("groups", ctypes.c_int64),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "fa_last_error": (ctypes.c_char_p, []),
+    "fa_version": (ctypes.c_char_p, []),
+    "fa_w8a8_gemm": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_w8a8_gemm_quantized": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_w8a8_gemm_partials": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
+    "fa_quantize_activations": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_rms_norm": (_i, [_p, _p, _p, _i, _i, _f, _p]),
+    "fa_rms_norm_quant": (_i, [_p, _p, _f, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "fa_silu": (_i, [_p, _i64, _p]),
+    "fa_mul": (_i, [_p, _p, _i64, _p]),
+    "fa_residual_add": (_i, [_p, _p, _i64, _p]),
+    "fa_silu_mul_quant": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "fa_quantize_weights_groupwise": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),
+    "fa_workspace_reserve": (_i, [_i, _i, _i, _i, _p]),
+    "fa_workspace_release": (_i, []),
+    "fa_bin_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
+    "fa_bin_close": (None, [_p]),
+    "fa_bin_num_tensors": (_i, [_p]),
+    "fa_bin_tensor_at": (_i, [_p, _i, ctypes.POINTER(TensorInfo)]),
+    "fa_bin_find": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
+    "fa_bin_quant_meta": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(QuantMeta)]),
+    "fa_infer_group_size": (_i, [_i64, _i, _i64]),
+}
+
+_LIB = None
+
+
+class FaError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("fish_w8a8 error %d: %s" % (code, msg))
+        self.code = code
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                "libfish_w8a8.so is not built (%s); run __graft_entry__.build()" % LIB_PATH)
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = l
+    return _LIB
+
+
+def check(rc):
+    if rc != FA_OK:
+        raise FaError(rc, lib().fa_last_error().decode())
+    return rc

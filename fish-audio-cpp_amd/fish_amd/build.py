@@ -1,0 +1,68 @@
+"""Builds the HIP library (gfx950) and the CPU oracle, in-tree.
+
+`build_library()` compiles every source under ``fish-audio-cpp_amd/csrc`` with
+hipcc into ``fish-audio-cpp_amd/lib/libfish_w8a8.so``.  `build_oracle()` runs
+``make`` in ``oracle/`` (the test checker, built next to the product but never
+linked into it).
+"""
+import os
+import subprocess
+import sys
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))  # fish-audio-cpp_amd/
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+LIB_DIR = os.path.join(PKG_ROOT, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libfish_w8a8.so")
+ORACLE_DIR = os.path.join(REPO_ROOT, "oracle")
+ORACLE_LIB = os.path.join(ORACLE_DIR, "_build", "liboracle_w8a8.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -ffp-contract=off: every FMA in the kernels is written as __builtin_fmaf, so
+# the rounding sequence is the one the code states.  Packed fp32 ops are off
+# (they have produced silent wrong results on these boxes).
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+HIP_SOURCES = ["quant.hip", "gemv.hip", "gemm.hip"]
+HOST_SOURCES = ["api.cpp", "loader.cpp", "kernels_cxx.cpp"]
+
+
+def _run(cmd, cwd=None):
+    res = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError("build failed: %s\n%s" % (" ".join(cmd), out))
+    return out
+
+
+def build_library(verbose=False):
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [HIPCC] + HIP_FLAGS + ["-I", os.path.join(PKG_ROOT, "include")]
+    cmd += [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    cmd += ["-x", "hip"] + [os.path.join(CSRC, s) for s in HOST_SOURCES]
+    cmd += ["-o", tmp]
+    out = _run(cmd)
+    os.replace(tmp, LIB_PATH)
+    if verbose and out.strip():
+        print(out)
+    return LIB_PATH
+
+
+def build_oracle(verbose=False):
+    out = _run(["make", "-s", "-C", ORACLE_DIR])
+    if verbose and out.strip():
+        print(out)
+    return ORACLE_LIB
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))
+    print(build_oracle(verbose=True))
+    sys.exit(0)

@@ -1,0 +1,144 @@
+"""PyTorch-tensor front end of the C ABI.
+
+torch supplies device memory and the current HIP stream; all arithmetic runs
+in libfish_w8a8.so.  Shapes follow the reference kernel API
+(src/kernels/kernels.h:242-259): W [M, K] int8, w_scale fp16 [M] or [M, G],
+X [N, K] fp16, returned Y is [N, M] fp16 (= the reference's col-major [M, N]).
+"""
+import torch
+
+from ._lib import check, lib
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _need(t, dtype, name):
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise ValueError("%s must be a device tensor" % name)
+    if t.dtype != dtype:
+        raise ValueError("%s must be %s, got %s" % (name, dtype, t.dtype))
+    if not t.is_contiguous():
+        raise ValueError("%s must be contiguous" % name)
+
+
+def num_groups(K, group_size):
+    g = K if group_size <= 0 or group_size > K else group_size
+    return (K + g - 1) // g
+
+
+def w8a8_gemm(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=None):
+    """int8_dequant_gemm_fp16: Y[n, m] for X fp16 [N, K] and W int8 [M, K]."""
+    _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale"); _need(X, torch.float16, "X")
+    _need(act_scale, torch.float16, "act_scale"); _need(smooth_inv, torch.float16, "smooth_inv")
+    M, K = W.shape
+    N = X.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=X.device)
+    check(lib().fa_w8a8_gemm(_ptr(W), _ptr(w_scale), group_size, _ptr(act_scale), _ptr(smooth_inv),
+                             _ptr(X), _ptr(Y), M, N, K, _stream()))
+    return Y
+
+
+def w8a8_gemm_quantized(W, w_scale, group_size, X_q, X_scale, out=None):
+    _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale")
+    _need(X_q, torch.int8, "X_q"); _need(X_scale, torch.float32, "X_scale")
+    M, K = W.shape
+    N = X_q.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=X_q.device)
+    check(lib().fa_w8a8_gemm_quantized(_ptr(W), _ptr(w_scale), group_size, _ptr(X_q), _ptr(X_scale),
+                                       _ptr(Y), M, N, K, _stream()))
+    return Y
+
+
+def w8a8_gemm_partials(W, w_scale, group_size, X_q, X_scale, row0=0, rows=None, tok0=0, toks=None):
+    """Y plus the exact int32 partials [toks, rows, G] of the window."""
+    M, K = W.shape
+    N = X_q.shape[0]
+    rows = M - row0 if rows is None else rows
+    toks = N - tok0 if toks is None else toks
+    G = num_groups(K, group_size)
+    Y = torch.empty((N, M), dtype=torch.float16, device=X_q.device)
+    P = torch.full((toks, rows, G), -2**31, dtype=torch.int32, device=X_q.device)
+    check(lib().fa_w8a8_gemm_partials(_ptr(W), _ptr(w_scale), group_size, _ptr(X_q), _ptr(X_scale),
+                                      _ptr(Y), _ptr(P), row0, rows, tok0, toks, M, N, K, _stream()))
+    return Y, P
+
+
+def quantize_activations(X, group_size, act_scale=None, smooth_inv=None):
+    _need(X, torch.float16, "X")
+    N, K = X.shape
+    G = num_groups(K, group_size)
+    X_q = torch.empty((N, K), dtype=torch.int8, device=X.device)
+    X_s = torch.empty((N, G), dtype=torch.float32, device=X.device)
+    check(lib().fa_quantize_activations(_ptr(X), _ptr(act_scale), _ptr(smooth_inv), _ptr(X_q),
+                                        _ptr(X_s), N, K, group_size, _stream()))
+    return X_q, X_s
+
+
+def rms_norm(x, weight, eps):
+    _need(x, torch.float16, "x"); _need(weight, torch.float16, "weight")
+    n, d = x.shape
+    out = torch.empty_like(x)
+    check(lib().fa_rms_norm(_ptr(x), _ptr(weight), _ptr(out), n, d, eps, _stream()))
+    return out
+
+
+def rms_norm_quant(x, weight, eps, group_size, smooth_inv=None, act_scale=None, want_out=False):
+    _need(x, torch.float16, "x"); _need(weight, torch.float16, "weight")
+    n, d = x.shape
+    G = num_groups(d, group_size)
+    X_q = torch.empty((n, d), dtype=torch.int8, device=x.device)
+    X_s = torch.empty((n, G), dtype=torch.float32, device=x.device)
+    out = torch.empty_like(x) if want_out else None
+    check(lib().fa_rms_norm_quant(_ptr(x), _ptr(weight), eps, _ptr(smooth_inv), _ptr(act_scale),
+                                  group_size, _ptr(X_q), _ptr(X_s), _ptr(out), n, d, _stream()))
+    return (X_q, X_s, out) if want_out else (X_q, X_s)
+
+
+def silu_(x):
+    _need(x, torch.float16, "x")
+    check(lib().fa_silu(_ptr(x), x.numel(), _stream()))
+    return x
+
+
+def mul_(a, b):
+    _need(a, torch.float16, "a"); _need(b, torch.float16, "b")
+    check(lib().fa_mul(_ptr(a), _ptr(b), a.numel(), _stream()))
+    return a
+
+
+def residual_add_(a, b):
+    _need(a, torch.float16, "a"); _need(b, torch.float16, "b")
+    check(lib().fa_residual_add(_ptr(a), _ptr(b), a.numel(), _stream()))
+    return a
+
+
+def silu_mul_quant(gate, up, group_size, smooth_inv=None, act_scale=None, want_out=False):
+    _need(gate, torch.float16, "gate"); _need(up, torch.float16, "up")
+    n, d = gate.shape
+    G = num_groups(d, group_size)
+    X_q = torch.empty((n, d), dtype=torch.int8, device=gate.device)
+    X_s = torch.empty((n, G), dtype=torch.float32, device=gate.device)
+    out = torch.empty_like(gate) if want_out else None
+    check(lib().fa_silu_mul_quant(_ptr(gate), _ptr(up), _ptr(smooth_inv), _ptr(act_scale),
+                                  group_size, _ptr(X_q), _ptr(X_s), _ptr(out), n, d, _stream()))
+    return (X_q, X_s, out) if want_out else (X_q, X_s)
+
+
+def quantize_weights_groupwise(w, group_size):
+    """tools/quant_utils.py quantize_groupwise on the device -> (q int8, scale fp16 [rows, G])."""
+    _need(w, torch.float16, "w")
+    rows, K = w.shape
+    G = (K + group_size - 1) // group_size
+    q = torch.empty((rows, K), dtype=torch.int8, device=w.device)
+    s = torch.empty((rows, G), dtype=torch.float16, device=w.device)
+    check(lib().fa_quantize_weights_groupwise(_ptr(w), rows, K, group_size, _ptr(q), _ptr(s),
+                                              _stream()))
+    return q, s

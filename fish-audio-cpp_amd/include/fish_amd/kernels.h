@@ -1,0 +1,41 @@
+// kernels.h -- C++ mirror of the reference's kernel API for the W8A8 path
+// (src/kernels/kernels.h:11-19, 111-140, 242-259), on HIP.
+//
+// Same names, argument order and meaning; hipStream_t replaces cudaStream_t,
+// and the cublasHandle_t slot of int8_dequant_gemm_fp16 becomes an unused
+// opaque pointer.  Failures throw std::runtime_error, as CUDA_CHECK does
+// (src/utils/cuda_utils.h:10-17).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace fish::kernels {
+
+void rms_norm(const __half* x, const __half* weight, __half* out, int n_tokens, int dim,
+              float eps, hipStream_t stream = 0);
+
+void silu_forward(__half* x, int n, hipStream_t stream = 0);
+void mul_forward(__half* a, const __half* b, int n, hipStream_t stream = 0);
+void residual_add(__half* a, const __half* b, int n, hipStream_t stream = 0);
+
+// W [M, K] int8 row-major; scale fp16 [M] or [M, G]; act_scale fp16 [G] or
+// null (dynamic); smooth_inv fp16 [K] or null; X fp16 [N, K] row-major;
+// Y fp16 col-major [M, N] (ld = M).
+void int8_dequant_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                            const __half* act_scale, const __half* smooth_inv, const __half* X,
+                            __half* Y, int M, int N, int K, void* blas_handle_unused,
+                            hipStream_t stream = 0);
+
+// Additive fused entry points (no single reference counterpart).
+void rms_norm_quant(const __half* x, const __half* weight, float eps, const __half* smooth_inv,
+                    const __half* act_scale, int group_size, int8_t* X_q, float* X_scale,
+                    __half* out, int n_tokens, int dim, hipStream_t stream = 0);
+void silu_mul_quant(const __half* gate, const __half* up, const __half* smooth_inv,
+                    const __half* act_scale, int group_size, int8_t* X_q, float* X_scale,
+                    __half* out, int n_tokens, int dim, hipStream_t stream = 0);
+void int8_gemm_quantized_fp16(const int8_t* W, const __half* scale, int group_size,
+                              const int8_t* X_q, const float* X_scale, __half* Y, int M, int N,
+                              int K, hipStream_t stream = 0);
+
+}  // namespace fish::kernels

@@ -1,0 +1,173 @@
+/*
+ * fish_w8a8.h -- C ABI of the MI355X-native W8A8 linear-layer path.
+ *
+ * Drop-in boundary for fish-audio-cpp's int8 linear layers.  Every entry point
+ * takes plain device pointers and sizes, enqueues work on `stream` (a
+ * hipStream_t; NULL is the default stream) and returns 0 (FA_OK) or a nonzero
+ * fa_status; fa_last_error() then describes the failure for the calling
+ * thread.  No entry point synchronises the stream, except that growing the
+ * per-thread scratch (see fa_workspace_reserve) waits for `stream` once.
+ *
+ * Index names follow the reference kernel API (src/kernels/kernels.h:242-259):
+ *   M = output features (rows of the int8 weight W [M, K], row-major),
+ *   N = tokens,  K = input features.
+ *   X  fp16 [N, K] row-major;  Y fp16 col-major [M, N] (= row-major [N, M]).
+ *   w_scale fp16 [M] (one group) or [M, G] row-major, G = ceil(K / group_size);
+ *   group_size <= 0 or > K means one group of K (int8_gemm.cu:396).
+ * fp16 buffers are passed as uint16_t bit patterns.
+ */
+#ifndef FISH_W8A8_H
+#define FISH_W8A8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    FA_OK = 0,
+    FA_ERR_INVALID_ARG = 1, /* null pointer, bad size or unsupported shape      */
+    FA_ERR_HIP = 2,         /* a HIP runtime call or kernel launch failed        */
+    FA_ERR_IO = 3,          /* .bin file could not be opened / mapped            */
+    FA_ERR_FORMAT = 4,      /* .bin file is malformed (magic, version, bounds)   */
+    FA_ERR_NOT_FOUND = 5    /* tensor name not present in the .bin file          */
+} fa_status;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* fa_last_error(void);
+/* Library version string. */
+const char* fa_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* W8A8 linear layer.                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces fish::kernels::int8_dequant_gemm_fp16 (src/kernels/kernels.h:249-259,
+ * src/kernels/int8_gemm.cu:384-511): quantize X per (token, K-group) to int8
+ * (dynamic amax/127 scales, or the static fp16 act_scale [G] when non-NULL;
+ * X * smooth_inv [K] first when non-NULL), exact int32 per-group dot products
+ * with W, fp32 dequant-sum over groups, fp16 Y.  The cublasHandle_t argument
+ * of the reference has no counterpart. */
+int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
+                 const uint16_t* act_scale, const uint16_t* smooth_inv,
+                 const uint16_t* X, uint16_t* Y, int M, int N, int K, void* stream);
+
+/* The same linear layer on activations that are already quantized (X_q int8
+ * [N, K] row-major, X_scale fp32 [N, G]): the part of int8_gemm.cu:423-505
+ * after its quantizer launch (:415-421).  Used after the fused prologues
+ * below. */
+int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_size,
+                           const int8_t* X_q, const float* X_scale, uint16_t* Y,
+                           int M, int N, int K, void* stream);
+
+/* Verification hook with no reference counterpart (the reference keeps its
+ * int32 partials inside cuBLAS, int8_gemm.cu:476-488): runs exactly the kernel
+ * fa_w8a8_gemm_quantized would run for this shape, writes Y, and also writes
+ * the exact int32 partial of every (token, row, group) in the window
+ * [tok0, tok0+toks) x [row0, row0+rows) to
+ * partials[((tok - tok0) * rows + (row - row0)) * G + group]. */
+int fa_w8a8_gemm_partials(const int8_t* W, const uint16_t* w_scale, int group_size,
+                          const int8_t* X_q, const float* X_scale, uint16_t* Y,
+                          int32_t* partials, int row0, int rows, int tok0, int toks,
+                          int M, int N, int K, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Activation quantizer and fused prologues.                                 */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_activation_groups_kernel (src/kernels/int8_gemm.cu:147-211):
+ * X fp16 [N, K] -> X_q int8 [N, K], X_scale fp32 [N, G]. */
+int fa_quantize_activations(const uint16_t* X, const uint16_t* act_scale,
+                            const uint16_t* smooth_inv, int8_t* X_q, float* X_scale,
+                            int N, int K, int group_size, void* stream);
+
+/* fish::kernels::rms_norm (src/kernels/kernels.h:11-19, rms_norm.cu:60-76). */
+int fa_rms_norm(const uint16_t* x, const uint16_t* weight, uint16_t* out,
+                int n_tokens, int dim, float eps, void* stream);
+
+/* rms_norm fused with the activation quantizer: the two launches the
+ * reference makes before wqkv and w1/w3 (dual_ar_engine.cc:580-583, 636-643)
+ * in one kernel.  out (the fp16 normalised rows) may be NULL. */
+int fa_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
+                      const uint16_t* smooth_inv, const uint16_t* act_scale, int group_size,
+                      int8_t* X_q, float* X_scale, uint16_t* out,
+                      int n_tokens, int dim, void* stream);
+
+/* fish::kernels::silu_forward / mul_forward / residual_add
+ * (src/kernels/kernels.h:111-140, ffn_activations.cu:139-161), in place on x/a. */
+int fa_silu(uint16_t* x, int64_t n, void* stream);
+int fa_mul(uint16_t* a, const uint16_t* b, int64_t n, void* stream);
+int fa_residual_add(uint16_t* a, const uint16_t* b, int64_t n, void* stream);
+
+/* silu(gate) * up (each rounded to fp16, as silu_forward then mul_forward)
+ * fused with the activation quantizer that feeds w2
+ * (dual_ar_engine.cc:640-646).  gate/up fp16 [n_tokens, dim]; out (the fp16
+ * product) may be NULL. */
+int fa_silu_mul_quant(const uint16_t* gate, const uint16_t* up,
+                      const uint16_t* smooth_inv, const uint16_t* act_scale, int group_size,
+                      int8_t* X_q, float* X_scale, uint16_t* out,
+                      int n_tokens, int dim, void* stream);
+
+/* Group-wise symmetric weight quantizer, tools/quant_utils.py:171-194
+ * quantize_groupwise, on the device: fp16 w [rows, K] -> int8 q [rows, K],
+ * fp16 scale [rows, G] (G = ceil(K / group_size), group_size > 0). */
+int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, int group_size,
+                                  int8_t* q, uint16_t* scale, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Scratch.                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Pre-size this thread's scratch on the current device for calls up to the
+ * given shape, so later calls never allocate (the reference grows its
+ * thread_local workspace with cudaMalloc inside the call,
+ * int8_gemm.cu:31-44, 97-102, 405-413).  Calls on one thread share the
+ * scratch: calls from one thread on two streams that overlap in time race. */
+int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_size,
+                         void* stream);
+/* Release this thread's scratch on the current device (waits for the device). */
+int fa_workspace_release(void);
+
+/* ------------------------------------------------------------------------ */
+/* dual_ar.bin container (src/model/tensor.h:8-67, src/model/loader.cc).     */
+/* ------------------------------------------------------------------------ */
+
+typedef struct fa_bin fa_bin;
+
+typedef struct {
+    char name[256];
+    uint32_t dtype;      /* 0 FP32, 1 FP16, 2 BF16, 3 INT8 (tensor.h:8-13) */
+    uint32_t ndim;
+    int64_t shape[8];
+    uint64_t offset;     /* byte offset of the data in the file */
+    uint64_t size;       /* byte count of the data */
+    const void* data;    /* host pointer into the read-only mapping */
+} fa_tensor_info;
+
+/* Companions of one int8 weight, as DualAREngine::init finds them
+ * (src/engine/dual_ar_engine.cc:231-275): <w>_scale, <w>_smooth_inv and
+ * <w>_act_scale; group_size inferred from the scale shape (:17-24). */
+typedef struct {
+    int has_scale, has_smooth_inv, has_act_scale;
+    int group_size;      /* 0 when the weight has no scale (fp16 weight) */
+    int64_t M, K;        /* weight rows and row length */
+    int64_t groups;      /* G as stored in the scale tensor */
+} fa_quant_meta;
+
+/* ModelLoader::load (loader.cc:50-152): mmap + header parse.  Also checks that
+ * every tensor's data lies inside the file. */
+int fa_bin_open(const char* path, fa_bin** out);
+void fa_bin_close(fa_bin* bin);
+int fa_bin_num_tensors(const fa_bin* bin);
+int fa_bin_tensor_at(const fa_bin* bin, int index, fa_tensor_info* info);
+/* ModelLoader::get / has (loader.cc:155-170); FA_ERR_NOT_FOUND if absent. */
+int fa_bin_find(const fa_bin* bin, const char* name, fa_tensor_info* info);
+int fa_bin_quant_meta(const fa_bin* bin, const char* weight_name, fa_quant_meta* meta);
+/* infer_group_size_from_scale (dual_ar_engine.cc:17-24). */
+int fa_infer_group_size(int64_t K, int scale_ndim, int64_t scale_groups);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,220 @@
+"""numpy front end of the C oracle (oracle/w8a8_ref.c).  TEST INFRASTRUCTURE.
+
+fp16 arrays are passed as numpy float16 (bit patterns are identical to the
+uint16 the C code takes).  Index names follow the reference API: M = output
+rows, N = tokens, K = input features; Y is returned as [N, M].
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle_w8a8.so")
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_SIGS = {
+    "orc_h2f": (_f, [ctypes.c_uint16]),
+    "orc_f2h": (ctypes.c_uint16, [_f]),
+    "orc_h2f_array": (None, [_p, _p, _i64]),
+    "orc_f2h_array": (None, [_p, _p, _i64]),
+    "orc_effective_group": (_i, [_i, _i]),
+    "orc_num_groups": (_i, [_i, _i]),
+    "orc_infer_group_size": (_i, [_i64, _i, _i64]),
+    "orc_quantize_weights_groupwise": (None, [_p, _i64, _i64, _i, _p, _p]),
+    "orc_quantize_activations": (None, [_p, _p, _p, _i, _i, _i, _p, _p]),
+    "orc_group_partials": (None, [_p, _p, _i, _i, _i, _i, _p]),
+    "orc_gemm_quantized": (None, [_p, _p, _i, _p, _p, _p, _i, _i, _i]),
+    "orc_w8a8_gemm": (None, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i]),
+    "orc_rms_inv": (_f, [_f, _i, _f]),
+    "orc_rms_norm": (None, [_p, _p, _p, _i, _i, _f]),
+    "orc_rms_norm_quant": (None, [_p, _p, _f, _p, _p, _i, _p, _p, _p, _i, _i]),
+    "orc_silu": (None, [_p, _i64]),
+    "orc_mul": (None, [_p, _p, _i64]),
+    "orc_residual_add": (None, [_p, _p, _i64]),
+    "orc_silu_mul_quant": (None, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i]),
+    "orc_num_threads": (_i, []),
+    "orc_set_num_threads": (None, [_i]),
+}
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("oracle not built: run `make -C oracle`")
+        l = ctypes.CDLL(LIB_PATH)
+        for k, (r, a) in _SIGS.items():
+            fn = getattr(l, k)
+            fn.restype = r
+            fn.argtypes = a
+        _LIB = l
+    return _LIB
+
+
+def _c(a, dtype):
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def groups(K, g):
+    return lib().orc_num_groups(K, g)
+
+
+def eff_group(K, g):
+    return lib().orc_effective_group(K, g)
+
+
+def f2h(x):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.float16)
+    lib().orc_f2h_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def h2f(h):
+    h = _c(h, np.float16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_h2f_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def quantize_weights(w, group_size):
+    w = _c(w, np.float16)
+    rows, K = w.shape
+    G = (K + group_size - 1) // group_size
+    q = np.empty((rows, K), np.int8)
+    s = np.empty((rows, G), np.float16)
+    lib().orc_quantize_weights_groupwise(_ptr(w), rows, K, group_size, _ptr(q), _ptr(s))
+    return q, s
+
+
+def quantize_activations(X, group_size, act_scale=None, smooth_inv=None):
+    X = _c(X, np.float16)
+    N, K = X.shape
+    G = groups(K, group_size)
+    xq = np.empty((N, K), np.int8)
+    xs = np.empty((N, G), np.float32)
+    act_scale = _c(act_scale, np.float16)
+    smooth_inv = _c(smooth_inv, np.float16)
+    lib().orc_quantize_activations(_ptr(X), _ptr(act_scale), _ptr(smooth_inv), N, K, group_size,
+                                   _ptr(xq), _ptr(xs))
+    return xq, xs
+
+
+def group_partials(W, xq, group_size):
+    W = _c(W, np.int8)
+    xq = _c(xq, np.int8)
+    M, K = W.shape
+    N = xq.shape[0]
+    G = groups(K, group_size)
+    P = np.empty((N, M, G), np.int32)
+    lib().orc_group_partials(_ptr(W), _ptr(xq), M, N, K, group_size, _ptr(P))
+    return P
+
+
+def gemm_quantized(W, w_scale, group_size, xq, xs):
+    W = _c(W, np.int8)
+    w_scale = _c(w_scale, np.float16)
+    xq = _c(xq, np.int8)
+    xs = _c(xs, np.float32)
+    M, K = W.shape
+    N = xq.shape[0]
+    Y = np.empty((N, M), np.float16)
+    lib().orc_gemm_quantized(_ptr(W), _ptr(w_scale), group_size, _ptr(xq), _ptr(xs), _ptr(Y), M, N, K)
+    return Y
+
+
+def w8a8_gemm(W, w_scale, group_size, X, act_scale=None, smooth_inv=None):
+    W = _c(W, np.int8)
+    w_scale = _c(w_scale, np.float16)
+    X = _c(X, np.float16)
+    act_scale = _c(act_scale, np.float16)
+    smooth_inv = _c(smooth_inv, np.float16)
+    M, K = W.shape
+    N = X.shape[0]
+    Y = np.empty((N, M), np.float16)
+    lib().orc_w8a8_gemm(_ptr(W), _ptr(w_scale), group_size, _ptr(act_scale), _ptr(smooth_inv),
+                        _ptr(X), _ptr(Y), M, N, K)
+    return Y
+
+
+def rms_norm(x, w, eps):
+    x = _c(x, np.float16)
+    w = _c(w, np.float16)
+    n, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_rms_norm(_ptr(x), _ptr(w), _ptr(out), n, d, eps)
+    return out
+
+
+def rms_norm_quant(x, w, eps, group_size, smooth_inv=None, act_scale=None):
+    x = _c(x, np.float16)
+    w = _c(w, np.float16)
+    n, d = x.shape
+    G = groups(d, group_size)
+    xq = np.empty((n, d), np.int8)
+    xs = np.empty((n, G), np.float32)
+    out = np.empty_like(x)
+    smooth_inv = _c(smooth_inv, np.float16)
+    act_scale = _c(act_scale, np.float16)
+    lib().orc_rms_norm_quant(_ptr(x), _ptr(w), eps, _ptr(smooth_inv), _ptr(act_scale), group_size,
+                             _ptr(xq), _ptr(xs), _ptr(out), n, d)
+    return xq, xs, out
+
+
+def silu(x):
+    x = np.array(x, dtype=np.float16, copy=True)
+    lib().orc_silu(_ptr(x), x.size)
+    return x
+
+
+def mul(a, b):
+    a = np.array(a, dtype=np.float16, copy=True)
+    b = _c(b, np.float16)
+    lib().orc_mul(_ptr(a), _ptr(b), a.size)
+    return a
+
+
+def residual_add(a, b):
+    a = np.array(a, dtype=np.float16, copy=True)
+    b = _c(b, np.float16)
+    lib().orc_residual_add(_ptr(a), _ptr(b), a.size)
+    return a
+
+
+def silu_mul_quant(gate, up, group_size, smooth_inv=None, act_scale=None):
+    gate = _c(gate, np.float16)
+    up = _c(up, np.float16)
+    n, d = gate.shape
+    G = groups(d, group_size)
+    xq = np.empty((n, d), np.int8)
+    xs = np.empty((n, G), np.float32)
+    out = np.empty_like(gate)
+    smooth_inv = _c(smooth_inv, np.float16)
+    act_scale = _c(act_scale, np.float16)
+    lib().orc_silu_mul_quant(_ptr(gate), _ptr(up), _ptr(smooth_inv), _ptr(act_scale), group_size,
+                             _ptr(xq), _ptr(xs), _ptr(out), n, d)
+    return xq, xs, out
+
+
+def rms_inv(sum_sq, dim, eps):
+    return lib().orc_rms_inv(sum_sq, dim, eps)
+
+
+def num_threads():
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n):
+    lib().orc_set_num_threads(n)

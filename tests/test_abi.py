@@ -1,0 +1,87 @@
+"""The C-ABI library loads, exports every declared symbol, and rejects bad
+arguments before touching the device (no GPU needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from fish_amd import _lib
+from fish_amd.build import LIB_PATH, REPO_ROOT
+
+HEADER = os.path.join(REPO_ROOT, "include", "fish_w8a8.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exists_and_loads():
+    assert os.path.exists(LIB_PATH), "run __graft_entry__.build() first"
+    l = _lib.lib()
+    assert l.fa_version().decode().startswith("fish-w8a8-mi355x")
+
+
+def test_every_declared_symbol_is_exported():
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    l = ctypes.CDLL(LIB_PATH)
+    missing = [s for s in syms if not hasattr(l, s)]
+    assert not missing, missing
+    # and the binding table covers exactly the header
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_cpp_mirror_symbols_exported():
+    out = subprocess.run(["nm", "-D", "-C", "--defined-only", LIB_PATH], stdout=subprocess.PIPE,
+                         text=True, check=True).stdout
+    for name in ["fish::kernels::int8_dequant_gemm_fp16", "fish::kernels::rms_norm",
+                 "fish::kernels::silu_forward", "fish::kernels::mul_forward",
+                 "fish::kernels::residual_add", "fish::ModelLoader::load",
+                 "fish::ModelLoader::get", "fish::infer_group_size_from_scale"]:
+        assert name in out, name
+
+
+def test_invalid_arguments_rejected_without_device():
+    l = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    # null pointers
+    rc = l.fa_w8a8_gemm(None, None, 64, None, None, None, None, 8, 1, 64, None)
+    assert rc == _lib.FA_ERR_INVALID_ARG
+    assert "null pointer" in l.fa_last_error().decode()
+    # K must be positive, M/N non-negative
+    assert l.fa_w8a8_gemm(dummy, dummy, 64, None, None, dummy, dummy, 8, 1, 0, None) == 1
+    assert l.fa_w8a8_gemm(dummy, dummy, 64, None, None, dummy, dummy, -1, 1, 64, None) == 1
+    assert l.fa_w8a8_gemm_quantized(dummy, dummy, 64, dummy, dummy, dummy, 8, -2, 64, None) == 1
+    # empty batch is a no-op (nothing is launched)
+    assert l.fa_w8a8_gemm(dummy, dummy, 64, None, None, dummy, dummy, 8, 0, 64, None) == 0
+    assert l.fa_w8a8_gemm_quantized(dummy, dummy, 64, dummy, dummy, dummy, 0, 4, 64, None) == 0
+    # partials window outside the problem
+    rc = l.fa_w8a8_gemm_partials(dummy, dummy, 64, dummy, dummy, dummy, dummy, 0, 9, 0, 1,
+                                 8, 1, 64, None)
+    assert rc == 1 and "window" in l.fa_last_error().decode()
+    assert l.fa_rms_norm(dummy, dummy, dummy, 1, 0, 1e-6, None) == 1
+    assert l.fa_rms_norm(dummy, dummy, dummy, 1, 70000, 1e-6, None) == 1
+    assert l.fa_rms_norm_quant(dummy, dummy, 1e-6, None, None, 64, None, None, None, 1, 64,
+                               None) == 1
+    assert l.fa_silu(None, 4, None) == 1
+    assert l.fa_silu(None, 0, None) == 0
+    assert l.fa_mul(dummy, None, 4, None) == 1
+    assert l.fa_quantize_weights_groupwise(dummy, 4, 64, 0, dummy, dummy, None) == 1
+    assert l.fa_quantize_activations(None, None, None, None, None, 1, 64, 64, None) == 1
+    # a successful call clears the message
+    assert l.fa_silu(None, 0, None) == 0
+    assert l.fa_last_error().decode() == ""
+
+
+def test_infer_group_size():
+    l = _lib.lib()
+    # src/engine/dual_ar_engine.cc:17-24
+    assert l.fa_infer_group_size(2560, 1, 1) == 2560
+    assert l.fa_infer_group_size(2560, 2, 1) == 2560
+    assert l.fa_infer_group_size(2560, 2, 10) == 256
+    assert l.fa_infer_group_size(9728, 2, 152) == 64
+    assert l.fa_infer_group_size(100, 2, 3) == 34

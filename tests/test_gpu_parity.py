@@ -1,0 +1,303 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bar: int8 activations, activation scales, weight quantization, RMSNorm and the
+elementwise ops are bit-exact; every int32 per-group partial is bit-exact; the
+prefill GEMM's fp16 output is bit-exact (it sums groups in the oracle's
+order); the decode GEMV's fp16 output, whose fp32 group sum is split across
+waves, is within 1 fp16 ulp or rtol 1e-3 (assert_fp16_close).
+"""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+from fish_amd import ops, synth
+from fish_amd.binfile import BinFile, write_bin
+from helpers import assert_fp16_close
+
+pytestmark = pytest.mark.gpu
+
+LAYER = synth.LAYER_SHAPES
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    assert torch.cuda.is_available(), "GPU tests need a device"
+    from fish_amd import _lib
+    _lib.lib()   # fails loudly when the HIP library is missing
+    ref.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype, (a.shape, b.shape, a.dtype, b.dtype)
+    return np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def make_linear(M, K, g, seed=0):
+    """W fp16 ~ N(0, 0.02) quantized group-wise by the oracle -> (q, scale)."""
+    w = synth.weights_f16(M, K, seed=seed)
+    ge = K if g <= 0 or g > K else g
+    return ref.quantize_weights(w, ge)
+
+
+# ------------------------------------------------------- quantizers ----
+
+@pytest.mark.parametrize("N,K,g", [(1, 2560, 256), (8, 2560, 64), (16, 512, 64), (5, 100, 48),
+                                   (3, 96, 0), (2, 4096, 5000), (7, 9728, 64), (4, 24, 8)])
+@pytest.mark.parametrize("variant", ["dynamic", "static", "smooth"])
+def test_quantize_activations_bitexact(N, K, g, variant):
+    x = synth.activations_f16(N, K, seed=K + N)
+    G = ref.groups(K, g)
+    act = np.abs(synth.activations_f16(1, G, seed=9)[0]) * np.float16(0.05) if variant == "static" else None
+    sm = synth.gamma_f16(K, seed=5) if variant == "smooth" else None
+    xq, xs = ops.quantize_activations(dev(x), g, act_scale=None if act is None else dev(act),
+                                      smooth_inv=None if sm is None else dev(sm))
+    rq, rs = ref.quantize_activations(x, g, act_scale=act, smooth_inv=sm)
+    assert same(host(xq), rq)
+    assert same(host(xs), rs)
+
+
+@pytest.mark.parametrize("rows,K,g", [(64, 512, 64), (37, 100, 48), (128, 2560, 256), (5, 64, 1000)])
+def test_quantize_weights_bitexact(rows, K, g):
+    w = synth.weights_f16(rows, K, seed=rows)
+    w[1] = 0
+    q, s = ops.quantize_weights_groupwise(dev(w), g)
+    rq, rs = ref.quantize_weights(w, g)
+    assert same(host(q), rq) and same(host(s), rs)
+
+
+@pytest.mark.parametrize("n,dim", [(4, 8), (1, 4), (3, 16), (2, 100), (3, 1000), (5, 2560),
+                                   (2, 4096), (1, 9728)])
+def test_rms_norm_bitexact(n, dim):
+    x = synth.activations_f16(n, dim, seed=dim)
+    w = synth.gamma_f16(dim)
+    out = ops.rms_norm(dev(x), dev(w), 1e-6)
+    assert same(host(out), ref.rms_norm(x, w, 1e-6))
+
+
+def test_rms_norm_reference_closed_forms():
+    # tests/test_kernels.cu:121-210 through the device kernel
+    out = host(ops.rms_norm(dev(np.ones((4, 8), np.float16)), dev(np.ones(8, np.float16)), 1e-6))
+    assert np.all(np.abs(out.astype(np.float32) - 1) <= 1e-3)
+    out = host(ops.rms_norm(dev(np.zeros((2, 4), np.float16)), dev(np.ones(4, np.float16)), 1e-5))
+    assert np.all(np.isfinite(out.astype(np.float32)))
+    x = np.array([[1, 3, 1, 3]], np.float16)
+    out = host(ops.rms_norm(dev(x), dev(np.full(4, 2, np.float16)), 1e-6)).astype(np.float64)
+    assert np.all(np.abs(out - 2 * x / np.sqrt(5 + 1e-6)) <= 1e-2)
+
+
+@pytest.mark.parametrize("n,dim,g", [(8, 2560, 64), (1, 2560, 256), (3, 100, 48), (2, 4096, 0)])
+@pytest.mark.parametrize("variant", ["dynamic", "static", "smooth"])
+def test_rms_norm_quant_bitexact(n, dim, g, variant):
+    x = synth.activations_f16(n, dim, seed=n)
+    w = synth.gamma_f16(dim)
+    G = ref.groups(dim, g)
+    act = np.full(G, 0.03, np.float16) if variant == "static" else None
+    sm = synth.gamma_f16(dim, seed=4) if variant == "smooth" else None
+    xq, xs, out = ops.rms_norm_quant(dev(x), dev(w), 1e-6, g, smooth_inv=None if sm is None else dev(sm),
+                                     act_scale=None if act is None else dev(act), want_out=True)
+    rq, rs, rout = ref.rms_norm_quant(x, w, 1e-6, g, smooth_inv=sm, act_scale=act)
+    assert same(host(out), rout)
+    assert same(host(xq), rq)
+    assert same(host(xs), rs)
+
+
+def test_elementwise_bitexact():
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal(100003) * 4).astype(np.float16)
+    b = rng.standard_normal(100003).astype(np.float16)
+    assert same(host(ops.silu_(dev(a))), ref.silu(a))
+    assert same(host(ops.mul_(dev(a), dev(b))), ref.mul(a, b))
+    assert same(host(ops.residual_add_(dev(a), dev(b))), ref.residual_add(a, b))
+    # tests/test_kernels.cu:355-379, 432-481 closed forms
+    x = np.arange(-8, 8).astype(np.float16)
+    got = host(ops.silu_(dev(x))).astype(np.float64)
+    assert np.all(np.abs(got - x / (1 + np.exp(-x.astype(np.float64)))) <= 1e-2)
+
+
+@pytest.mark.parametrize("n,dim,g", [(8, 9728, 64), (1, 9728, 256), (2, 100, 48)])
+def test_silu_mul_quant_bitexact(n, dim, g):
+    rng = np.random.default_rng(dim)
+    gate = (rng.standard_normal((n, dim)) * 3).astype(np.float16)
+    up = rng.standard_normal((n, dim)).astype(np.float16)
+    xq, xs, out = ops.silu_mul_quant(dev(gate), dev(up), g, want_out=True)
+    rq, rs, rout = ref.silu_mul_quant(gate, up, g)
+    assert same(host(out), rout)
+    assert same(host(xq), rq)
+    assert same(host(xs), rs)
+
+
+# --------------------------------------------------------- linear ----
+
+def check_linear(N, M, K, g, seed=0, full_entry=True):
+    """Partials bit-exact, Y within the path's tolerance (bit-exact on the
+    GEMM path).  Returns the device Y."""
+    q, s = make_linear(M, K, g, seed=seed)
+    if s.shape[1] == 1:
+        s = s[:, 0]
+    x = synth.activations_f16(N, K, seed=seed + 1)
+    rq, rs = ref.quantize_activations(x, g)
+    Wd, Sd = dev(q), dev(s)
+    Y, P = ops.w8a8_gemm_partials(Wd, Sd, g, dev(rq), dev(rs))
+    rP = ref.group_partials(q, rq, g)
+    assert same(host(P), rP), "int32 partials differ"
+    rY = ref.gemm_quantized(q, s, g, rq, rs)
+    if N > 16 and K % 64 == 0 and (g if 0 < g <= K else K) % 64 == 0:
+        assert same(host(Y), rY), "GEMM path must match the oracle bit for bit"
+    else:
+        assert_fp16_close(host(Y), rY, "Y N=%d M=%d K=%d g=%d" % (N, M, K, g))
+    if full_entry:
+        Y2 = ops.w8a8_gemm(Wd, Sd, dev(x), g)
+        assert_fp16_close(host(Y2), ref.w8a8_gemm(q, s, g, x), "fa_w8a8_gemm")
+        # the whole entry point runs the same kernels as the partials hook
+        assert same(host(Y2), host(Y))
+    return Y
+
+
+def test_config0_plumbing_m16_k512_n512_g64():
+    """16 tokens, K=512, 512 outputs, g64, seed 0."""
+    check_linear(16, 512, 512, 64, seed=0)
+
+
+@pytest.mark.parametrize("name", list(LAYER))
+def test_config1_decode_m1_g256(name):
+    K, Nout = LAYER[name]
+    check_linear(1, Nout, K, 256, seed=1)
+
+
+@pytest.mark.parametrize("name", list(LAYER))
+def test_config2_decode_m8_g64_fused_prologue(name):
+    """8 tokens, g64, activation quant fused with RMSNorm (qkv,
+    gate_up), SiLU*mul (down) or plain (o)."""
+    K, Nout = LAYER[name]
+    g, n = 64, 8
+    q, s = make_linear(Nout, K, g, seed=2)
+    if name in ("qkv", "gate_up"):
+        x = synth.activations_f16(n, K, seed=3)
+        gam = synth.gamma_f16(K)
+        xq, xs = ops.rms_norm_quant(dev(x), dev(gam), 1e-6, g)
+        rq, rs, _ = ref.rms_norm_quant(x, gam, 1e-6, g)
+    elif name == "down":
+        rng = np.random.default_rng(4)
+        gate = (rng.standard_normal((n, K)) * 2).astype(np.float16)
+        up = rng.standard_normal((n, K)).astype(np.float16)
+        xq, xs = ops.silu_mul_quant(dev(gate), dev(up), g)
+        rq, rs, _ = ref.silu_mul_quant(gate, up, g)
+    else:
+        x = synth.activations_f16(n, K, seed=5)
+        xq, xs = ops.quantize_activations(dev(x), g)
+        rq, rs = ref.quantize_activations(x, g)
+    assert same(host(xq), rq) and same(host(xs), rs)
+    Y, P = ops.w8a8_gemm_partials(dev(q), dev(s), g, xq, xs)
+    assert same(host(P), ref.group_partials(q, rq, g))
+    assert_fp16_close(host(Y), ref.gemm_quantized(q, s, g, rq, rs), name)
+
+
+def test_config3_prefill_m512_qkv_bitexact():
+    K, Nout = LAYER["qkv"]
+    check_linear(512, Nout, K, 256, seed=6, full_entry=False)
+
+
+@pytest.mark.parametrize("name", list(LAYER))
+def test_config3_prefill_m2048_g256_subblock(name):
+    """configs[3] at M=2048: int32 per-group partials bit-exact on a 64x64
+    output sub-block, fp16 outputs bit-exact on sampled rows x tokens."""
+    K, Nout = LAYER[name]
+    N, g = 2048, 256
+    torch.manual_seed(0)
+    w = (torch.randn(Nout, K, device="cuda") * 0.02).half()
+    Wd, Sd = ops.quantize_weights_groupwise(w, g)
+    x = (torch.randn(N, K, device="cuda")).half()
+    xq, xs = ops.quantize_activations(x, g)
+    r0, t0 = (Nout // 3) // 16 * 16 + 5, 1000 + 3
+    Y, P = ops.w8a8_gemm_partials(Wd, Sd, g, xq, xs, row0=r0, rows=64, tok0=t0, toks=64)
+    q, s, hq, hs, hY, hP = (host(t) for t in (Wd, Sd, xq, xs, Y, P))
+    rP = ref.group_partials(q[r0:r0 + 64], hq[t0:t0 + 64], g)
+    assert same(hP, rP)
+    rows = np.unique(np.concatenate([np.arange(0, Nout, 97), [Nout - 1]]))
+    toks = np.unique(np.concatenate([np.arange(0, N, 61), [N - 1]]))
+    rY = ref.gemm_quantized(q[rows], s[rows], g, hq[toks], hs[toks])
+    assert same(hY[np.ix_(toks, rows)], rY)
+
+
+@pytest.mark.parametrize("N,M,K,g", [
+    (1, 100, 512, 64),      # partial 16-row tile
+    (16, 48, 64, 64),       # one K step
+    (3, 16, 4096, 4096),    # g == K (one group, 1-D scale)
+    (2, 40, 128, 0),        # group_size <= 0 -> K
+    (1, 40, 128, 1000),     # group_size > K  -> K
+    (4, 64, 1024, 128),     # g128: two MFMA steps per group
+    (17, 130, 256, 128),    # first GEMM size, ragged tiles
+    (300, 200, 512, 512),   # GEMM, ragged tokens
+    (3, 40, 100, 48),       # K, g not multiples of 64: generic kernel
+    (20, 33, 96, 32),       # generic kernel, N > 16
+])
+def test_edge_shapes(N, M, K, g):
+    check_linear(N, M, K, g, seed=N + M)
+
+
+def test_unaligned_weight_uses_exact_path():
+    M, K, g, N = 24, 256, 64, 2
+    q, s = make_linear(M, K, g, seed=11)
+    x = synth.activations_f16(N, K, seed=12)
+    buf = torch.zeros(M * K + 16, dtype=torch.int8, device="cuda")
+    Wd = buf[1:1 + M * K].view(M, K)
+    Wd.copy_(dev(q))
+    Y = ops.w8a8_gemm(Wd, dev(s), dev(x), g)
+    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x), "unaligned")
+
+
+def test_static_and_smooth_through_entry_point():
+    M, K, g, N = 256, 512, 64, 4
+    q, s = make_linear(M, K, g, seed=13)
+    x = synth.activations_f16(N, K, seed=14)
+    act = np.full(K // g, 0.04, np.float16)
+    sm = synth.gamma_f16(K, seed=15)
+    Y = ops.w8a8_gemm(dev(q), dev(s), dev(x), g, act_scale=dev(act), smooth_inv=dev(sm))
+    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x, act_scale=act, smooth_inv=sm), "static")
+
+
+def test_gemv_deterministic_and_counters_rearmed():
+    """Split-K GEMV: repeated calls, other shapes in between, identical Y."""
+    K, Nout = LAYER["down"]
+    q, s = make_linear(Nout, K, 256, seed=21)
+    x = synth.activations_f16(1, K, seed=22)
+    Wd, Sd, Xd = dev(q), dev(s), dev(x)
+    first = host(ops.w8a8_gemm(Wd, Sd, Xd, 256))
+    for _ in range(3):
+        check_linear(2, 48, 512, 64, seed=3, full_entry=False)
+        again = host(ops.w8a8_gemm(Wd, Sd, Xd, 256))
+        assert same(first, again)
+
+
+def test_bin_file_end_to_end():
+    """int8 weight + fp16 scale written in the dual_ar.bin layout, read back by
+    the library's loader, group size inferred from the scale shape, run."""
+    K, Nout, g = 2560, 512, 64
+    q, s = make_linear(Nout, K, g, seed=31)
+    name = "text_model.model.layers.0.attention.wqkv.weight"
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "dual_ar.bin")
+        write_bin(path, [(name, q), (name + "_scale", s)])
+        with BinFile(path) as b:
+            meta = b.quant_meta(name)
+            assert meta.group_size == g and meta.has_scale
+            Wd, Sd = dev(b.array(name)), dev(b.array(name + "_scale"))
+    x = synth.activations_f16(1, K, seed=32)
+    Y = ops.w8a8_gemm(Wd, Sd, dev(x), meta.group_size)
+    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x), "bin")
