@@ -2,10 +2,12 @@
 // management and kernel dispatch.
 //
 // Dispatch for the linear layer (reference dispatcher: int8_gemm.cu:384-511):
-//   K % 64 == 0, group % 64 == 0, 16-byte aligned W and X_q:
-//       N <= 16  -> decode GEMV on int8 MFMA (gemv.hip), split over K-groups
-//       N  > 16  -> LDS-tiled int8 MFMA GEMM (gemm.hip)
+//   16-byte aligned W and X_q, N <= 16 and a shape plan_gemv takes:
+//       N == 1        -> v_dot4 GEMV, one wave per 1-2 weight rows (gemv.hip)
+//       2 <= N <= 16  -> int8 MFMA GEMV, 16-row tiles (gemv.hip)
+//   aligned, K % 64 == 0, group % 64 == 0 -> LDS-tiled int8 MFMA GEMM (gemm.hip)
 //   anything else -> the exact any-shape kernel (gemm.hip, generic)
+// All paths sum the K-groups in the same order, so they agree bit for bit.
 // The error convention mirrors CUDA_CHECK (src/utils/cuda_utils.h:10-17): a
 // failing HIP call is reported with file/line and hipGetErrorString, here as
 // a status code plus a per-thread message instead of an exception.
@@ -48,10 +50,6 @@ struct Workspace {
     size_t xq_bytes = 0;
     float* xs = nullptr;
     size_t xs_bytes = 0;
-    float* part = nullptr;
-    size_t part_bytes = 0;
-    int* counters = nullptr;
-    size_t counter_count = 0;
 };
 
 thread_local std::unordered_map<int, Workspace> g_ws;
@@ -77,53 +75,21 @@ int grow(void** p, size_t* have, size_t need, hipStream_t stream) {
     return FA_OK;
 }
 
-int grow_counters(Workspace& ws, size_t count, hipStream_t stream) {
-    if (ws.counter_count >= count) return FA_OK;
-    size_t bytes_have = ws.counter_count * sizeof(int);
-    void* p = ws.counters;
-    int rc = grow(&p, &bytes_have, count * sizeof(int), stream);
-    if (rc) return rc;
-    ws.counters = (int*)p;
-    ws.counter_count = bytes_have / sizeof(int);
-    // Counters start at zero; the GEMV re-arms each one after use.
-    FA_HIP(hipMemset(ws.counters, 0, bytes_have));
-    return FA_OK;
-}
-
 int eff_group(int K, int g) { return (g <= 0 || g > K) ? K : g; }
-
-bool fast_shape(const int8_t* W, const int8_t* xq, int K, int g) {
-    return (K % 64 == 0) && (g % 64 == 0) && aligned16(W) && aligned16(xq);
-}
-
-// Worst-case split-K scratch (floats) of the GEMV for N tokens and M rows.
-size_t gemv_part_floats(int M, int N, int K, int g, int G) {
-    fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
-    return p.splits > 1 ? (size_t)p.splits * (size_t)N * (size_t)M : 0;
-}
 
 int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, int g, int G,
                      const int8_t* xq, const float* xs, uint16_t* Y, int32_t* dbg, int row0,
                      int rows, int tok0, int toks, int M, int N, int K, hipStream_t stream) {
-    if (fast_shape(W, xq, K, g)) {
-        if (N <= 16) {
-            fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
-            Workspace* ws = nullptr;
-            int rc = current_ws(&ws);
-            if (rc) return rc;
-            if (p.splits > 1) {
-                void* part = ws->part;
-                rc = grow(&part, &ws->part_bytes,
-                          (size_t)p.splits * (size_t)N * (size_t)M * sizeof(float), stream);
-                ws->part = (float*)part;
-                if (rc) return rc;
-                rc = grow_counters(*ws, (size_t)p.tiles, stream);
-                if (rc) return rc;
-            }
-            FA_HIP(fa::launch_gemv(p, W, w_scale, xq, xs, Y, ws->part, ws->counters, dbg, row0,
+    const bool aligned = aligned16(W) && aligned16(xq);
+    if (aligned && N <= 16) {
+        fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
+        if (p.kind != 0) {
+            FA_HIP(fa::launch_gemv(p, W, w_scale, xq, xs, nullptr, nullptr, nullptr, Y, dbg, row0,
                                    rows, tok0, toks, M, N, K, g, G, stream));
             return FA_OK;
         }
+    }
+    if (aligned && K % 64 == 0 && g % 64 == 0) {
         FA_HIP(fa::launch_gemm(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g, G,
                                stream));
         return FA_OK;
@@ -200,6 +166,15 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W)) {
+        // decode: the GEMV quantizes the token itself (one launch, no scratch)
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G);
+        if (gp.kind == 1 || gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, X, act_scale, smooth_inv, Y,
+                                   nullptr, 0, 0, 0, 0, M, N, K, g, G, s));
+            return FA_OK;
+        }
+    }
     Workspace* ws = nullptr;
     rc = current_ws(&ws);
     if (rc) return rc;
@@ -337,19 +312,7 @@ int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_siz
     rc = grow(&p, &ws->xs_bytes, (size_t)max_tokens * (size_t)G * sizeof(float), s);
     ws->xs = (float*)p;
     if (rc) return rc;
-    // GEMV split scratch: splits * M is at most (2560 + tiles) * 16 for any M.
-    const int n16 = max_tokens < 16 ? max_tokens : 16;
-    size_t worst = 0;
-    for (int m = 16; m <= max_M + 15; m += 16) {
-        size_t f = gemv_part_floats(m, n16, max_K, g, G);
-        if (f > worst) worst = f;
-        if (m > 65536) break;
-    }
-    p = ws->part;
-    rc = grow(&p, &ws->part_bytes, worst * sizeof(float), s);
-    ws->part = (float*)p;
-    if (rc) return rc;
-    return grow_counters(*ws, (size_t)fa::ceil_div(max_M > 0 ? max_M : 1, 16), s);
+    return FA_OK;
 }
 
 int fa_workspace_release(void) {
@@ -360,8 +323,6 @@ int fa_workspace_release(void) {
     FA_HIP(hipDeviceSynchronize());
     if (ws->xq) FA_HIP(hipFree(ws->xq));
     if (ws->xs) FA_HIP(hipFree(ws->xs));
-    if (ws->part) FA_HIP(hipFree(ws->part));
-    if (ws->counters) FA_HIP(hipFree(ws->counters));
     *ws = Workspace{};
     return FA_OK;
 }

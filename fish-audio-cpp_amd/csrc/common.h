@@ -82,22 +82,32 @@ hipError_t launch_elementwise(int op, uint16_t* a, const uint16_t* b, int64_t n,
 hipError_t launch_quantize_weights(const uint16_t* w, int64_t rows, int64_t K, int g,
                                    int8_t* q, uint16_t* scale, hipStream_t stream);
 
-// Decode GEMV (N <= 16 tokens) on int8 MFMA.  part/counters: split-K scratch.
+// Decode GEMV (N <= 16 tokens): a v_dot4 kernel for N == 1 and an int8 MFMA
+// kernel for 2 <= N <= 16.  kind == 0 means "shape not taken".
 struct GemvPlan {
-    int tiles;   // ceil(M / 16)
-    int splits;  // K-group splits across workgroups
-    int gps;     // groups per split
+    int kind = 0;    // 1, 2: dot kernel with 1 or 2 rows per wave; 3: MFMA kernel
+                     // (dot: grid = row blocks, capped at launch to the resident count)
+    int kd = 0;      // dot: passes in flight per wave
+    int lg = 0;      // dot: log2(group size)
+    int passes = 0;  // dot: passes per row
+    int spg = 0;     // mfma: 64-byte K steps per group
+    int maxg = 0;    // mfma: groups per wave (register-resident terms)
+    int grid = 0, block = 0;
+    size_t lds = 0;
 };
 GemvPlan plan_gemv(int M, int N, int K, int g, int G);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
 // [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to
 // dbg_partials[((tok - dbg_tok0) * dbg_rows + (row - dbg_row0)) * G + group].
+// With X non-null (dot kernel only) the kernel quantizes the fp16 token X
+// itself (act_scale / smooth_inv as in launch_quantize_activations) and
+// ignores x_q / x_scale.
 hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
-                       const int8_t* x_q, const float* x_scale, uint16_t* Y, float* part,
-                       int* counters, int32_t* dbg_partials, int dbg_row0, int dbg_rows,
-                       int dbg_tok0, int dbg_toks, int M, int N, int K, int g, int G,
-                       hipStream_t stream);
+                       const int8_t* x_q, const float* x_scale, const uint16_t* X,
+                       const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
+                       int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
+                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream);
 
 // Prefill GEMM on int8 MFMA with LDS-staged tiles.
 hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,

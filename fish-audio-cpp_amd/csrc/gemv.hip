@@ -1,221 +1,544 @@
-// gemv.hip -- decode-shaped W8A8 linear (N <= 16 tokens) on CDNA4 int8 MFMA.
+// gemv.hip -- decode-shaped W8A8 linear (N <= 16 tokens) for CDNA4.
 //
-// Replaces the reference's int8_matvec_dequant_kernel / int8_smallbatch
-// kernel and, for 5 <= N <= 16, its per-group cuBLAS loop
-// (src/kernels/int8_gemm.cu:245-380, 439-498).
+// Replaces the reference's int8_matvec_dequant_kernel (N == 1), its
+// small-batch kernel (2 <= N <= 4) and, for 5 <= N <= 16, its per-group
+// cuBLAS loop (src/kernels/int8_gemm.cu:245-380, 439-498).
 //
-// Shape of the work: one wave owns a tile of 16 weight rows and a contiguous
-// range of K-groups (a "split").  Each lane streams 16 bytes of one weight row
-// per 64-wide K step (lane -> row lane&15, byte offset 16*(lane>>4)), so a
-// wave reads 16 rows x 64 B per step with 128-bit loads.  The activations of
-// up to 16 tokens ride in the MFMA's second operand with the same byte
-// mapping, so v_mfma_i32_16x16x64_i8 yields the exact int32 dot product of
-// every (row, token) pair over those 64 bytes.  A K-group of g bytes is g/64
-// chained MFMAs; after its last one the int32 partial P_g is scaled in
-// registers: acc = fma(float(P_g) * w_scale, x_scale, acc) -- the order the
-// reference's accumulate kernel uses (int8_gemm.cu:231, contracted by nvcc).
+// Both kernels below form every int32 per-group partial P_g exactly and then
+// sum the groups in the reference accumulate kernel's order
+// (int8_gemm.cu:213-234, nvcc contracting `acc += float(P) * ws * xs` into
+// fma(float(P) * ws, xs, acc)), sequentially over g = 0, 1, ..., so the fp16
+// output is bit-identical to the host oracle.  Splitting K across waves only
+// changes who computes the terms float(P_g) * ws; the fma chain over the terms
+// runs in group order on one lane per output.
 //
-// Loads run two blocks of 8 K-steps ahead of the MFMAs (ping-pong register
-// buffers), and the split's weight/activation scales are staged in LDS once.
-// When a tile is split over several waves, each wave writes its fp32 partial
-// to scratch; the last wave to finish (per-tile arrival counter) adds the
-// partials in split order -- a fixed order, so results are deterministic --
-// writes fp16 and re-arms the counter for the next launch.
+// gemv_dot_kernel (N == 1): one wave streams R = 1 or 2 weight rows.  A row's
+// 64/R lanes each load 16 bytes per pass (128-bit loads, a pass covers
+// 1024/R contiguous bytes of the row) and form 4 v_dot4_i32_i8 products with
+// the activation bytes; lanes holding the same K-group (g/16 of them) add
+// their partials with cross-lane shuffles.  Up to KD passes are in flight per
+// wave (a register ring refilled as it drains); no split-K, so every CU keeps
+// dozens of independent row streams.
+//
+// gemv_mfma_kernel (2 <= N <= 16): a workgroup owns 16 weight rows; its NW
+// waves split the K-groups into contiguous ranges.  Lane l streams 16 bytes of
+// row l&15 at byte offset 16*(l>>4) of each 64-byte K step, the tokens' int8
+// activations ride in the second MFMA operand with the same byte mapping, so
+// v_mfma_i32_16x16x64_i8 yields the exact int32 dot of every (row, token) pair
+// over 64 bytes; g/64 chained MFMAs make P_g.  Terms are kept in registers;
+// afterwards the waves pass the running fp32 sums along in group order
+// through LDS.
 #include "common.h"
 
 namespace fa {
 namespace {
 
-constexpr int kRows = 16;         // weight rows per wave tile
-constexpr int kBlk = 8;           // K-steps (64 B each) per load block
-constexpr int kMaxGroupsPerWave = 64;
-
 struct DbgWindow {
     int32_t* p;
     int row0, rows, tok0, toks;
+    __device__ bool in(int row, int tok) const {
+        return p && row >= row0 && row < row0 + rows && tok >= tok0 && tok < tok0 + toks;
+    }
+    __device__ int32_t& at(int row, int tok, int gi, int G) const {
+        return p[((size_t)(tok - tok0) * rows + (row - row0)) * G + gi];
+    }
 };
 
 __device__ __forceinline__ v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 
-template <bool kDbg>
-__global__ __launch_bounds__(64) void gemv_mfma_kernel(
+// ------------------------------------------------------------ N == 1 ----
+
+constexpr int kDotWaves = 4;   // waves per workgroup
+
+// Sum of an int over aligned blocks of LG lanes (all lanes get the block sum).
+// LG <= 16 stays inside a 16-lane DPP row: quad_perm swaps, then half-row and
+// row mirrors, one v_add_*_dpp each.  Integer sums are exact in any order.
+template <int LG>
+__device__ __forceinline__ int group_sum(int p, int lg_rt) {
+    if constexpr (LG == 0) {
+        for (int off = 1; off < (1 << lg_rt); off <<= 1) p += __shfl_xor(p, off, 64);
+        return p;
+    } else {
+        if constexpr (LG >= 2) p += __builtin_amdgcn_update_dpp(0, p, 0xB1, 0xF, 0xF, false);
+        if constexpr (LG >= 4) p += __builtin_amdgcn_update_dpp(0, p, 0x4E, 0xF, 0xF, false);
+        if constexpr (LG >= 8) p += __builtin_amdgcn_update_dpp(0, p, 0x141, 0xF, 0xF, false);
+        if constexpr (LG >= 16) p += __builtin_amdgcn_update_dpp(0, p, 0x140, 0xF, 0xF, false);
+        if constexpr (LG >= 32) p += __shfl_xor(p, 16, 64);
+        if constexpr (LG >= 64) p += __shfl_xor(p, 32, 64);
+        return p;
+    }
+}
+
+// QX: the kernel quantizes the fp16 token itself (int8_gemm.cu:147-211
+// semantics: per-group amax/127 or a static scale, optional smooth_inv) while
+// the first weight loads are in flight; otherwise it stages the given int8
+// activations and fp32 scales.  Either way x_q [K] and x_scale [G] sit in LDS.
+//
+// Work: row blocks of kDotWaves * R rows; block b, b + gridDim.x, ... belong to
+// workgroup b.  A uniform cursor (row block, pass) walks the wave's passes in
+// order; the weight ring is KD passes ahead of the consumer.  g is a power of
+// two (lg_g = log2 g), so group indices are shifts.
+template <int R, int KD, int LG, bool QX, int XV>
+__global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
-    uint16_t* __restrict__ Y, float* __restrict__ part, int* __restrict__ counters,
-    DbgWindow dbg, int M, int N, int K, int g, int G, int tiles, int splits, int gps) {
-    __shared__ float ws_s[kRows * kMaxGroupsPerWave];
-    __shared__ float xs_s[kRows * kMaxGroupsPerWave];
-    __shared__ int s_last;
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ act_scale,
+    const uint16_t* __restrict__ smooth_inv,
+    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int K, int lg_g, int G, int passes,
+    int nblocks) {
+    constexpr int RL = 64 / R;            // lanes per row
+    constexpr int PB = RL * 16;           // bytes of a row per pass
+    constexpr int NT = kDotWaves * 64;
+    extern __shared__ __align__(16) float lds[];
+    const int Kp = (K + 15) & ~15;
+    int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                  // [Kp]
+    float* xs_s = lds + Kp / 4;                                      // [G]
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    float* terms = xs_s + G + wave * R * G;                          // [R][G]
+    int* gmax = reinterpret_cast<int*>(xs_s + G + kDotWaves * R * G);  // [G] (QX)
 
-    const int lane = threadIdx.x;
-    const int tile = blockIdx.x % tiles;
-    const int split = blockIdx.x / tiles;
-    const int g_begin = split * gps;
-    const int g_end = min(G, g_begin + gps);
-    const int ng = g_end - g_begin;
-    const int row0 = tile * kRows;
-    const int spg = g >> 6;               // MFMA K-steps per group
-    const int nsteps = ng * spg;
+    const int rsub = lane / RL;
+    const int li = lane % RL;
+    const int lane_k = li * 16;
+    const bool leader = (li & ((LG ? LG : 1) - 1)) == 0;
 
-    const int lr = lane & 15;             // A: weight row in tile; B: token
-    const int kq = (lane >> 4) * 16;      // byte offset inside a 64-B step
+    // ---- activation loads first: their wait then does not cover the ring.
+    // XV 16-byte chunks per thread (int8 codes, or 8 fp16 values with QX).
+    v4i xr[XV];
+    float xsr = 0.0f;
+    // (unconditional loads from clamped addresses: a load under a branch makes
+    // the compiler wait for it on the spot)
+    if constexpr (!QX) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int k = (tid + i * NT) * 16;
+            xr[i] = ld16(x_q + (k < Kp ? k : Kp - 16));
+        }
+        xsr = x_scale[tid < G ? tid : G - 1];
+    } else {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int k = (tid + i * NT) * 8;
+            xr[i] = *reinterpret_cast<const v4i*>(X + (k < K ? k : K - 8));
+        }
+    }
+
+    // ---- weight ring
+    int l_blk = blockIdx.x, l_pass = 0;     // load cursor (uniform)
+    const int8_t* const wlast = W + (size_t)(M - 1) * K;
+    v4i a[KD];
+    uint16_t sc[KD];
+    const v4i zero = {0, 0, 0, 0};
+    auto row_of_blk = [&](int blk) { return (blk * kDotWaves + wave) * R + rsub; };
+    auto load = [&](int slot) {
+        const bool live = l_blk < nblocks;
+        const int row = row_of_blk(live ? l_blk : blockIdx.x);
+        const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
+        const int k = l_pass * PB + lane_k;
+        const bool ok = live && k < K;
+        const int kk = ok ? k : 0;
+        const v4i wa = ld16(wrow + kk);
+        sc[slot] = w_scale[G == 1 ? (size_t)(row < M ? row : M - 1)
+                                  : (size_t)(row < M ? row : M - 1) * G + (kk >> lg_g)];
+        a[slot] = ok ? wa : zero;
+        if (++l_pass == passes) {
+            l_pass = 0;
+            l_blk += gridDim.x;
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < KD; ++s) load(s);
+
+    // ---- stage activations into LDS
+    if constexpr (!QX) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int k = (tid + i * NT) * 16;
+            if (k < Kp) *reinterpret_cast<v4i*>(xq_s + k) = xr[i];
+        }
+        if (tid < G) xs_s[tid] = xsr;
+        for (int k = (tid + XV * NT) * 16; k < Kp; k += NT * 16)   // K > 16 KB
+            *reinterpret_cast<v4i*>(xq_s + k) = ld16(x_q + k);
+        for (int i = tid + NT; i < G; i += NT) xs_s[i] = x_scale[i];
+    } else {
+        // per-group |v| maxima (exact in any order), scales, then int8 codes
+        for (int i = tid; i < G; i += NT) gmax[i] = 0;
+        __syncthreads();
+        auto vals = [&](int k, const v4i& raw, float (&v)[8]) {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = h2f(h[e]);
+                if (smooth_inv) v[e] *= h2f(smooth_inv[k + e]);
+            }
+        };
+        auto amax_chunk = [&](int k, const v4i& raw) {
+            float v[8];
+            vals(k, raw, v);
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+            atomicMax(&gmax[k >> lg_g], __float_as_int(m));   // |v| >= 0: int order == float order
+        };
+        auto quant_chunk = [&](int k, const v4i& raw) {
+            float v[8];
+            vals(k, raw, v);
+            const float inv = 1.0f / xs_s[k >> lg_g];
+            int q[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
+            uint2 u;
+            u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                  ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+            u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
+                  ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
+            *reinterpret_cast<uint2*>(xq_s + k) = u;
+        };
+        if (!act_scale) {
+#pragma unroll
+            for (int c = 0; c < XV; ++c) {
+                const int k = (tid + c * NT) * 8;
+                if (k < K) amax_chunk(k, xr[c]);
+            }
+            for (int k = (tid + XV * NT) * 8; k < K; k += NT * 8)
+                amax_chunk(k, *reinterpret_cast<const v4i*>(X + k));
+            __syncthreads();
+        }
+        for (int i = tid; i < G; i += NT) {
+            float s;
+            if (act_scale) {
+                s = h2f(act_scale[i]);
+                s = s < 1e-8f ? 1e-8f : s;
+            } else {
+                s = act_scale_from_amax(__int_as_float(gmax[i]));
+            }
+            xs_s[i] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < XV; ++c) {
+            const int k = (tid + c * NT) * 8;
+            if (k < K) quant_chunk(k, xr[c]);
+        }
+        for (int k = (tid + XV * NT) * 8; k < K; k += NT * 8)
+            quant_chunk(k, *reinterpret_cast<const v4i*>(X + k));
+    }
+    __syncthreads();
+
+    // ---- consume: per pass 4 v_dot4, a lane-group sum, one term per group
+    int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
+    auto consume = [&](int slot) {
+        const int k = c_pass * PB + lane_k;
+        const v4i b = *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
+        int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
+        p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
+        p = __builtin_amdgcn_sdot4(a[slot].z, b.z, p, false);
+        p = __builtin_amdgcn_sdot4(a[slot].w, b.w, p, false);
+        p = group_sum<LG>(p, lg_g - 4);
+        const int row = row_of_blk(c_blk);
+        const bool lead = LG ? leader : (li & ((1 << (lg_g - 4)) - 1)) == 0;
+        if (k < K && lead) {
+            const int gi = k >> lg_g;
+            terms[rsub * G + gi] = (float)p * h2f(sc[slot]);
+            if (dbg.p && row < M && dbg.in(row, 0)) dbg.at(row, 0, gi, G) = p;
+        }
+        if (++c_pass == passes) {
+            // Row done: the group-ordered fp32 chain on one lane per row.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (li == 0 && row < M) {
+                float acc = 0.0f;
+                const float* t = terms + rsub * G;
+#pragma unroll 8
+                for (int gi = 0; gi < G; ++gi) acc = __builtin_fmaf(t[gi], xs_s[gi], acc);
+                Y[row] = f2h(acc);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            c_pass = 0;
+            c_blk += gridDim.x;
+        }
+    };
+    // Rounds that refill the ring, then a last round that only drains it (so
+    // every load is unconditional and the wait counts stay exact).
+    const int my_blocks = (nblocks - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+    const int items = my_blocks * passes;
+    int base = 0;
+    for (; base + KD < items; base += KD) {
+#pragma unroll
+        for (int s = 0; s < KD; ++s) {
+            consume(s);
+            load(s);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < KD; ++s)
+        if (base + s < items) consume(s);
+}
+
+// ------------------------------------------------------ 2 <= N <= 16 ----
+
+constexpr int kTile = 16;
+
+template <int SPG, int MAXG, bool kDbg>
+__global__ __launch_bounds__(512) void gemv_mfma_kernel(
+    const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
+    const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
+    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G) {
+    constexpr int NSTEP = SPG * MAXG;
+    constexpr int KD = NSTEP < 8 ? NSTEP : 8;
+    extern __shared__ float lds[];
+    float* ws_s = lds;                   // [16 rows][G]
+    float* xs_s = lds + kTile * G;       // [16 tokens][G]
+    float* chain = lds + 2 * kTile * G;  // [16 tokens][16 rows]
+
+    const int NW = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * kTile;
+    const int gb = (wave * G) / NW;
+    const int ng = ((wave + 1) * G) / NW - gb;
+    const int nsteps = ng * SPG;
+
+    const int lr = lane & 15;            // A: weight row in tile; B: token
+    const int kq = (lane >> 4) * 16;
     const int row_ld = min(row0 + lr, M - 1);
     const bool tok_ok = lr < N;
-    const size_t kbase = (size_t)g_begin * g + kq;
+    const size_t kbase = (size_t)gb * SPG * 64 + kq;
     const int8_t* wp = W + (size_t)row_ld * K + kbase;
     const int8_t* xp = x_q + (size_t)(tok_ok ? lr : 0) * K + kbase;
 
-    v4i a0[kBlk], b0[kBlk], a1[kBlk], b1[kBlk];
+    v4i a[KD], b[KD];
     const v4i zero = {0, 0, 0, 0};
-
-    auto load_block = [&](v4i (&a)[kBlk], v4i (&b)[kBlk], int blk) {
-#pragma unroll
-        for (int s = 0; s < kBlk; ++s) {
-            const int step = blk * kBlk + s;
-            if (step < nsteps) {
-                a[s] = ld16(wp + (size_t)step * 64);
-                b[s] = tok_ok ? ld16(xp + (size_t)step * 64) : zero;
-            } else {
-                a[s] = zero;
-                b[s] = zero;
-            }
-        }
+    auto load = [&](int slot, int step) {
+        const size_t off = (size_t)(step < nsteps ? step : 0) * 64;
+        a[slot] = ld16(wp + off);
+        b[slot] = tok_ok ? ld16(xp + off) : zero;
     };
+#pragma unroll
+    for (int s = 0; s < KD; ++s) load(s, s);
 
-    load_block(a0, b0, 0);
-
-    // Stage this split's scales: w_scale rows of the tile, x_scale of the
-    // tokens (fp16 [M] when G == 1, reference int8_gemm.cu:228-230).
-    for (int i = lane; i < kRows * ng; i += 64) {
-        const int r = i / ng, j = i - r * ng;
+    for (int i = threadIdx.x; i < kTile * G; i += blockDim.x) {
+        const int r = i / G, gi = i - r * G;
         const int row = min(row0 + r, M - 1);
-        ws_s[r * kMaxGroupsPerWave + j] =
-            h2f(G == 1 ? w_scale[row] : w_scale[(size_t)row * G + g_begin + j]);
-        xs_s[r * kMaxGroupsPerWave + j] = r < N ? x_scale[(size_t)r * G + g_begin + j] : 0.0f;
+        ws_s[i] = h2f(G == 1 ? w_scale[row] : w_scale[(size_t)row * G + gi]);
+        xs_s[i] = r < N ? x_scale[(size_t)r * G + gi] : 0.0f;
     }
     __syncthreads();
 
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    v4i P = zero;
-    int sig = 0;   // steps done in the current group
-    int gj = 0;    // current group, relative to g_begin
-    const int orow = 4 * (lane >> 4);   // first of this lane's 4 output rows in the tile
-
-    auto compute_block = [&](const v4i (&a)[kBlk], const v4i (&b)[kBlk], int blk) {
+    const int orow = 4 * (lane >> 4);    // this lane's 4 output rows: orow .. orow+3
+    float terms[MAXG][4];
 #pragma unroll
-        for (int s = 0; s < kBlk; ++s) {
-            const int step = blk * kBlk + s;
-            if (step < nsteps) {
-                P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s], b[s], P, 0, 0, 0);
-                if (++sig == spg) {
-                    const float xs = xs_s[lr * kMaxGroupsPerWave + gj];
+    for (int j = 0; j < MAXG; ++j) {
+        v4i P = zero;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float ws = ws_s[(orow + r) * kMaxGroupsPerWave + gj];
-                        acc[r] = __builtin_fmaf((float)P[r] * ws, xs, acc[r]);
-                    }
-                    if constexpr (kDbg) {
-                        const int t = lr;
-                        if (t >= dbg.tok0 && t < dbg.tok0 + dbg.toks && t < N) {
+        for (int s = 0; s < SPG; ++s) {
+            const int step = j * SPG + s;
+            const int slot = step % KD;
+            P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], b[slot], P, 0, 0, 0);
+            load(slot, step + KD);
+        }
+        const int gi = gb + (j < ng ? j : 0);
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const int row = row0 + orow + r;
-                                if (row >= dbg.row0 && row < dbg.row0 + dbg.rows && row < M)
-                                    dbg.p[((size_t)(t - dbg.tok0) * dbg.rows + (row - dbg.row0)) *
-                                              G + g_begin + gj] = P[r];
-                            }
-                        }
-                    }
-                    P = zero;
-                    sig = 0;
-                    ++gj;
+        for (int r = 0; r < 4; ++r) terms[j][r] = (float)P[r] * ws_s[(orow + r) * G + gi];
+        if constexpr (kDbg) {
+            if (j < ng && lr < N) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + orow + r;
+                    if (row < M && dbg.in(row, lr)) dbg.at(row, lr, gb + j, G) = P[r];
                 }
             }
         }
-    };
-
-    const int nblk = (nsteps + kBlk - 1) / kBlk;
-    for (int blk = 0; blk < nblk; blk += 2) {
-        if (blk + 1 < nblk) load_block(a1, b1, blk + 1);
-        compute_block(a0, b0, blk);
-        if (blk + 2 < nblk) load_block(a0, b0, blk + 2);
-        if (blk + 1 < nblk) compute_block(a1, b1, blk + 1);
     }
 
-    const int t = lr;
-    if (splits == 1) {
-        if (t < N) {
+    // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
+    // the previous wave's sums over its own groups.
+    for (int w = 0; w < NW; ++w) {
+        if (wave == w) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = row0 + orow + r;
-                if (row < M) Y[(size_t)t * M + row] = f2h(acc[r]);
+                float acc = w == 0 ? 0.0f : chain[lr * kTile + orow + r];
+#pragma unroll
+                for (int j = 0; j < MAXG; ++j)
+                    if (j < ng) acc = __builtin_fmaf(terms[j][r], xs_s[lr * G + gb + j], acc);
+                chain[lr * kTile + orow + r] = acc;
             }
         }
-        return;
+        __syncthreads();
     }
+    for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
+        const int t = i / kTile, r = i - t * kTile;
+        if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
+    }
+}
 
-    if (t < N) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = row0 + orow + r;
-            if (row < M) part[((size_t)split * N + t) * M + row] = acc[r];
-        }
+// Host-side instantiation tables.
+using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*,
+                       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,
+                       int, int, int, int, int, int);
+
+template <int R, int KD, bool QX, int XV>
+DotFn dot_for_lg(int lg) {
+    switch (lg) {
+        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV>;
+        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV>;
+        default: return gemv_dot_kernel<R, KD, 0, QX, XV>;
     }
-    __threadfence();
-    if (lane == 0) s_last = atomicAdd(&counters[tile], 1) == splits - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (t < N) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = row0 + orow + r;
-            if (row < M) {
-                float s = 0.0f;
-                for (int sp = 0; sp < splits; ++sp) s += part[((size_t)sp * N + t) * M + row];
-                Y[(size_t)t * M + row] = f2h(s);
-            }
-        }
+}
+
+template <int R, bool QX, int XV>
+DotFn dot_for_kd(int kd, int lg) {
+    switch (kd) {
+        case 3: return dot_for_lg<R, 3, QX, XV>(lg);
+        case 4: return dot_for_lg<R, 4, QX, XV>(lg);
+        case 5: return dot_for_lg<R, 5, QX, XV>(lg);
+        case 8: return dot_for_lg<R, 8, QX, XV>(lg);
+        default: return dot_for_lg<R, 10, QX, XV>(lg);
     }
-    if (lane == 0) counters[tile] = 0;
+}
+
+// XV: activation chunks per thread, 1 or 3 for int8 codes (K <= 4096 / 12288),
+// 2 or 5 for fp16 input (K <= 4096 / 10240); larger K use a tail loop.
+template <int R>
+DotFn dot_for(bool qx, int K, int kd, int lg) {
+    if (qx) return K <= 4096 ? dot_for_kd<R, true, 2>(kd, lg) : dot_for_kd<R, true, 5>(kd, lg);
+    return K <= 4096 ? dot_for_kd<R, false, 1>(kd, lg) : dot_for_kd<R, false, 3>(kd, lg);
+}
+
+template <bool D>
+using MfmaFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*, uint16_t*,
+                        DbgWindow, int, int, int, int);
+
+template <int SPG, bool D>
+MfmaFn<D> mfma_for_maxg(int maxg) {
+    switch (maxg) {
+        case 1: return gemv_mfma_kernel<SPG, 1, D>;
+        case 2: return gemv_mfma_kernel<SPG, 2, D>;
+        case 3: return gemv_mfma_kernel<SPG, 3, D>;
+        case 4: return gemv_mfma_kernel<SPG, 4, D>;
+        case 6: return gemv_mfma_kernel<SPG, 6, D>;
+        case 8: return gemv_mfma_kernel<SPG, 8, D>;
+        case 12: return gemv_mfma_kernel<SPG, 12, D>;
+        case 16: return gemv_mfma_kernel<SPG, 16, D>;
+        default: return gemv_mfma_kernel<SPG, 20, D>;
+    }
+}
+
+template <bool D>
+MfmaFn<D> mfma_for(int spg, int maxg) {
+    switch (spg) {
+        case 1: return mfma_for_maxg<1, D>(maxg);
+        case 2: return mfma_for_maxg<2, D>(maxg);
+        case 4: return mfma_for_maxg<4, D>(maxg);
+        default: return mfma_for_maxg<8, D>(maxg);
+    }
+}
+
+int round_maxg(int m) {
+    static const int opts[] = {1, 2, 3, 4, 6, 8, 12, 16, 20};
+    for (int o : opts)
+        if (m <= o) return o;
+    return 20;
 }
 
 }  // namespace
 
 GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
-    (void)N;
-    (void)K;
-    (void)g;
-    GemvPlan p;
-    p.tiles = ceil_div(M, kRows);
-    // Aim for ~10 waves per CU over 256 CUs so every CU keeps several 16-row
-    // weight streams in flight; never split finer than one group per wave.
-    const int target_waves = 2560;
-    int s = target_waves / (p.tiles > 0 ? p.tiles : 1);
-    if (s < 1) s = 1;
-    if (s > G) s = G;
-    int gps = ceil_div(G, s);
-    if (gps > kMaxGroupsPerWave) gps = kMaxGroupsPerWave;
-    p.gps = gps;
-    p.splits = ceil_div(G, gps);
-    return p;
+    GemvPlan p{};
+    const bool pow2_lanes = g % 16 == 0 && ((g / 16) & (g / 16 - 1)) == 0;
+    if (N == 1 && pow2_lanes && K % 16 == 0 && K <= 32768) {
+        const int lgroups = g / 16;
+        p.kind = (M >= 4096 && lgroups <= 32) ? 2 : 1;   // rows per wave
+        const int R = p.kind;
+        if (lgroups > 64 / R) return GemvPlan{};
+        const int PB = (64 / R) * 16;
+        const int passes = (K + PB - 1) / PB;
+        // ring depth: every pass of a row in flight when it fits (items flow
+        // on into the next row either way)
+        static const int opts[] = {3, 4, 5, 8, 10};
+        p.kd = 10;
+        for (int o : opts)
+            if (o >= passes) {
+                p.kd = o;
+                break;
+            }
+        p.grid = ceil_div(M, kDotWaves * R);    // row blocks; capped at launch
+        p.block = kDotWaves * 64;
+        const int Kp = (K + 15) & ~15;
+        p.lds = (size_t)Kp + (size_t)(2 * G + kDotWaves * R * G) * sizeof(float);
+        if (g < 16) return GemvPlan{};
+        if (p.lds > 64 * 1024) return GemvPlan{};
+        int lg = 0;
+        while ((1 << lg) < g) ++lg;
+        p.lg = lg;            // log2(g)
+        p.passes = passes;
+        return p;
+    }
+    if (N >= 1 && N <= 16 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 64 == 0) {
+        const int tiles = ceil_div(M, kTile);
+        // waves per 16-row tile: enough for ~2048 waves in flight, at most 8,
+        // each holding at most 20 groups' terms in registers
+        int nw = ceil_div(2048, tiles);
+        if (nw < ceil_div(G, 20)) nw = ceil_div(G, 20);
+        if (nw > G) nw = G;
+        if (nw > 8) nw = 8;
+        if (ceil_div(G, nw) > 20) return GemvPlan{};
+        p.kind = 3;
+        p.spg = g / 64;
+        p.maxg = round_maxg(ceil_div(G, nw));
+        p.grid = tiles;
+        p.block = nw * 64;
+        p.lds = (size_t)(2 * kTile * G + kTile * kTile) * sizeof(float);
+        if (p.lds > 64 * 1024) return GemvPlan{};
+        return p;
+    }
+    return GemvPlan{};
+}
+
+int dot_resident_blocks(DotFn fn, size_t lds) {
+    int dev = 0, cus = 256, occ = 1;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kDotWaves * 64, lds) != hipSuccess ||
+        occ < 1)
+        occ = 1;
+    return cus * occ;
 }
 
 hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
-                       const int8_t* x_q, const float* x_scale, uint16_t* Y, float* part,
-                       int* counters, int32_t* dbg_partials, int dbg_row0, int dbg_rows,
-                       int dbg_tok0, int dbg_toks, int M, int N, int K, int g, int G,
-                       hipStream_t stream) {
+                       const int8_t* x_q, const float* x_scale, const uint16_t* X,
+                       const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
+                       int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
+                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
-    const dim3 grid((unsigned)(p.tiles * p.splits));
-    if (dbg_partials)
-        hipLaunchKernelGGL((gemv_mfma_kernel<true>), grid, dim3(64), 0, stream, W, w_scale, x_q,
-                           x_scale, Y, part, counters, dbg, M, N, K, g, G, p.tiles, p.splits,
-                           p.gps);
-    else
-        hipLaunchKernelGGL((gemv_mfma_kernel<false>), grid, dim3(64), 0, stream, W, w_scale, x_q,
-                           x_scale, Y, part, counters, dbg, M, N, K, g, G, p.tiles, p.splits,
-                           p.gps);
+    if (p.kind == 1 || p.kind == 2) {
+        const bool qx = X != nullptr;
+        const int lgl = p.lg - 4;   // log2(lanes per group)
+        DotFn fn = p.kind == 1 ? dot_for<1>(qx, K, p.kd, lgl) : dot_for<2>(qx, K, p.kd, lgl);
+        // as many workgroups as fit at once, each with the same number of
+        // row blocks (no straggler round)
+        const int cap = dot_resident_blocks(fn, p.lds);
+        const int per_wg = ceil_div(p.grid, cap);
+        const int grid = ceil_div(p.grid, per_wg);
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,
+                           X, act_scale, smooth_inv, Y, dbg, M, K, p.lg, G, p.passes, p.grid);
+    } else if (p.kind == 3) {
+        if (X) return hipErrorInvalidValue;
+        const bool d = dbg_partials != nullptr;
+        if (d)
+            hipLaunchKernelGGL(mfma_for<true>(p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
+                               stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
+        else
+            hipLaunchKernelGGL(mfma_for<false>(p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
+                               stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

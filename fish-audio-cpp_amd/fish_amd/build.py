@@ -42,14 +42,25 @@ def _run(cmd, cwd=None):
 
 
 def build_library(verbose=False):
+    """Compile each source to an object in parallel, then link the .so."""
+    from concurrent.futures import ThreadPoolExecutor
     os.makedirs(LIB_DIR, exist_ok=True)
+    obj_dir = os.path.join(PKG_ROOT, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+    inc = ["-I", os.path.join(PKG_ROOT, "include")]
+    flags = [f for f in HIP_FLAGS if f != "-shared"]
+    jobs = []
+    for src in HIP_SOURCES + HOST_SOURCES:
+        obj = os.path.join(obj_dir, src + ".o")
+        lang = [] if src.endswith(".hip") else ["-x", "hip"]
+        jobs.append((obj, [HIPCC] + flags + inc + ["-c"] + lang + [os.path.join(CSRC, src), "-o", obj]))
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        outs = list(ex.map(lambda j: _run(j[1]), jobs))
     tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC] + HIP_FLAGS + ["-I", os.path.join(PKG_ROOT, "include")]
-    cmd += [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    cmd += ["-x", "hip"] + [os.path.join(CSRC, s) for s in HOST_SOURCES]
-    cmd += ["-o", tmp]
-    out = _run(cmd)
+    outs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + [o for o, _ in jobs]
+                     + ["-o", tmp]))
     os.replace(tmp, LIB_PATH)
+    out = "\n".join(o for o in outs if o.strip())
     if verbose and out.strip():
         print(out)
     return LIB_PATH

@@ -1,10 +1,12 @@
 """GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
 
-Bar: int8 activations, activation scales, weight quantization, RMSNorm and the
-elementwise ops are bit-exact; every int32 per-group partial is bit-exact; the
-prefill GEMM's fp16 output is bit-exact (it sums groups in the oracle's
-order); the decode GEMV's fp16 output, whose fp32 group sum is split across
-waves, is within 1 fp16 ulp or rtol 1e-3 (assert_fp16_close).
+Bar: bit-exact everywhere.  int8 activations, activation scales, weight
+quantization, RMSNorm and the elementwise ops match the oracle bit for bit;
+every int32 per-group partial matches exactly; and every linear-layer path
+(decode GEMV, prefill GEMM, any-shape kernel) sums the K-groups in the
+oracle's order, so its fp16 output matches bit for bit as well -- stricter
+than the path's stated output tolerance of 1 fp16 ulp or rtol 1e-3, which
+the oracle itself is held to against float64 in test_oracle.py.
 """
 import os
 import tempfile
@@ -16,7 +18,6 @@ import torch
 from oracle import ref
 from fish_amd import ops, synth
 from fish_amd.binfile import BinFile, write_bin
-from helpers import assert_fp16_close
 
 pytestmark = pytest.mark.gpu
 
@@ -157,13 +158,10 @@ def check_linear(N, M, K, g, seed=0, full_entry=True):
     rP = ref.group_partials(q, rq, g)
     assert same(host(P), rP), "int32 partials differ"
     rY = ref.gemm_quantized(q, s, g, rq, rs)
-    if N > 16 and K % 64 == 0 and (g if 0 < g <= K else K) % 64 == 0:
-        assert same(host(Y), rY), "GEMM path must match the oracle bit for bit"
-    else:
-        assert_fp16_close(host(Y), rY, "Y N=%d M=%d K=%d g=%d" % (N, M, K, g))
+    assert same(host(Y), rY), "Y differs from the oracle (N=%d M=%d K=%d g=%d)" % (N, M, K, g)
     if full_entry:
         Y2 = ops.w8a8_gemm(Wd, Sd, dev(x), g)
-        assert_fp16_close(host(Y2), ref.w8a8_gemm(q, s, g, x), "fa_w8a8_gemm")
+        assert same(host(Y2), ref.w8a8_gemm(q, s, g, x)), "fa_w8a8_gemm"
         # the whole entry point runs the same kernels as the partials hook
         assert same(host(Y2), host(Y))
     return Y
@@ -205,7 +203,7 @@ def test_config2_decode_m8_g64_fused_prologue(name):
     assert same(host(xq), rq) and same(host(xs), rs)
     Y, P = ops.w8a8_gemm_partials(dev(q), dev(s), g, xq, xs)
     assert same(host(P), ref.group_partials(q, rq, g))
-    assert_fp16_close(host(Y), ref.gemm_quantized(q, s, g, rq, rs), name)
+    assert same(host(Y), ref.gemm_quantized(q, s, g, rq, rs)), name
 
 
 def test_config3_prefill_m512_qkv_bitexact():
@@ -259,7 +257,7 @@ def test_unaligned_weight_uses_exact_path():
     Wd = buf[1:1 + M * K].view(M, K)
     Wd.copy_(dev(q))
     Y = ops.w8a8_gemm(Wd, dev(s), dev(x), g)
-    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x), "unaligned")
+    assert same(host(Y), ref.w8a8_gemm(q, s, g, x)), "unaligned"
 
 
 def test_static_and_smooth_through_entry_point():
@@ -269,11 +267,11 @@ def test_static_and_smooth_through_entry_point():
     act = np.full(K // g, 0.04, np.float16)
     sm = synth.gamma_f16(K, seed=15)
     Y = ops.w8a8_gemm(dev(q), dev(s), dev(x), g, act_scale=dev(act), smooth_inv=dev(sm))
-    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x, act_scale=act, smooth_inv=sm), "static")
+    assert same(host(Y), ref.w8a8_gemm(q, s, g, x, act_scale=act, smooth_inv=sm)), "static"
 
 
-def test_gemv_deterministic_and_counters_rearmed():
-    """Split-K GEMV: repeated calls, other shapes in between, identical Y."""
+def test_gemv_deterministic_across_calls():
+    """Repeated calls with other shapes in between give identical Y."""
     K, Nout = LAYER["down"]
     q, s = make_linear(Nout, K, 256, seed=21)
     x = synth.activations_f16(1, K, seed=22)
@@ -300,4 +298,4 @@ def test_bin_file_end_to_end():
             Wd, Sd = dev(b.array(name)), dev(b.array(name + "_scale"))
     x = synth.activations_f16(1, K, seed=32)
     Y = ops.w8a8_gemm(Wd, Sd, dev(x), meta.group_size)
-    assert_fp16_close(host(Y), ref.w8a8_gemm(q, s, g, x), "bin")
+    assert same(host(Y), ref.w8a8_gemm(q, s, g, x)), "bin"
