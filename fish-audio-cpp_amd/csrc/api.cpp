@@ -89,6 +89,11 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
             return FA_OK;
         }
     }
+    if (aligned && fa::gemm_pipe_ok(M, N, K, g)) {
+        FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g,
+                                    G, stream));
+        return FA_OK;
+    }
     if (aligned && K % 64 == 0 && g % 64 == 0) {
         FA_HIP(fa::launch_gemm(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g, G,
                                stream));

@@ -115,6 +115,14 @@ hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x
                        int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g, int G,
                        hipStream_t stream);
 
+// Prefill GEMM with a direct-to-LDS multi-stage pipeline (K % 256 == 0,
+// g % 64 == 0).
+bool gemm_pipe_ok(int M, int N, int K, int g);
+hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                            const float* x_scale, uint16_t* Y, int32_t* dbg_partials, int dbg_row0,
+                            int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g,
+                            int G, hipStream_t stream);
+
 // Any-shape fallback (any K, any group size, unaligned pointers).
 hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                                const float* x_scale, uint16_t* Y, int32_t* dbg_partials,

@@ -31,6 +31,12 @@ constexpr int kStride = 80;    // LDS bytes per 64-byte K row (16 B pad)
 struct DbgWindow {
     int32_t* p;
     int row0, rows, tok0, toks;
+    __device__ bool in(int row, int tok) const {
+        return p && row >= row0 && row < row0 + rows && tok >= tok0 && tok < tok0 + toks;
+    }
+    __device__ int32_t& at(int row, int tok, int gi, int G) const {
+        return p[((size_t)(tok - tok0) * rows + (row - row0)) * G + gi];
+    }
 };
 
 __device__ __forceinline__ v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
@@ -199,6 +205,283 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(
         }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel (K % 256 == 0): kNst-deep LDS ring filled by direct
+// global->LDS loads.
+//
+// Workgroup tile BM weight rows x 128 tokens, 4 waves in 2 x 2, wave tile
+// (BM/2) x 64 = RB x 2 blocks of 32 x 32 (v_mfma_i32_32x32x32_i8).  Each
+// 64-byte K stage of the A and B tiles is loaded with global_load_lds_dwordx4
+// (no staging registers): load j of wave w fills the 64 consecutive 16-byte
+// LDS slots q = (4j + w) * 64 + lane, and slot q holds logical chunk
+// (q & 3) ^ ((row >> 2) & 3) of row q >> 2.  With that XOR swizzle the 16
+// lanes of a fragment read (16 rows, one chunk) hit 16 distinct 16-byte bank
+// groups.  The next group's scales ride one stage early in the same ring as
+// raw dwords (global_load_lds_dword) and are converted to fp32 once per group.
+//
+// The loads are issued from inline asm and waited for with explicit
+// s_waitcnt vmcnt(N): the compiler cannot tell which ring slot a direct-to-LDS
+// load writes and would otherwise drain every load before each LDS read.
+// Per stage and wave: AJ + BJ + 2 loads; waiting for stage s leaves the
+// (kNst - 2) younger stages in flight.  One barrier per stage; loads for stage
+// s + kNst - 1 are issued right after it into the slot all waves just left.
+//
+// Workgroups are dealt round-robin over the 8 XCDs; tile t is mapped so each
+// XCD runs a contiguous, row-block-major run of tiles and a weight-row block
+// is fetched into one XCD's L2 and reused by all of its token tiles.
+constexpr int kBN = 128;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+// Direct-to-LDS loads: lane i's data lands at lds + i * size.  m0 holds the
+// wave-uniform LDS base; no compiler-generated code in these kernels uses m0.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+// Same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane offset
+// (no per-load 64-bit address arithmetic in VGPRs).
+__device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+template <int BM, int KS, int kNst, int kOcc, bool kDbg>
+__global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
+    const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
+    const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
+    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int lg_spg, int G, int tiles_m,
+    int tiles_n) {
+    constexpr int RB = BM / 64;              // 32-row blocks per wave
+    constexpr int AJ = BM / 64;              // A loads per wave per 64-byte substep
+    constexpr int BJ = kBN / 64;             // B loads per wave per substep
+    constexpr int kPerStage = KS * (AJ + BJ + 2);
+    constexpr int kYounger = (kNst - 2) * kPerStage;
+    __shared__ __align__(16) int8_t As[kNst][KS][BM * 64];
+    __shared__ __align__(16) int8_t Bs[kNst][KS][kBN * 64];
+    __shared__ __align__(16) uint32_t wsr[kNst][KS][256];   // raw scale dwords
+    __shared__ __align__(16) float xsr[kNst][KS][256];
+    __shared__ __align__(16) float ws_f[4][BM];             // converted, ring by group & 3
+    __shared__ __align__(16) float xs_f[4][kBN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1;
+    const int wn = wave >> 1;
+
+    const int ntiles = tiles_m * tiles_n;
+    const int b = blockIdx.x;
+    int t = b;
+    if (ntiles % 8 == 0) t = (b % 8) * (ntiles / 8) + b / 8;
+    const int tm = t / tiles_n;
+    const int tn = t % tiles_n;
+    const int m0 = tm * BM;
+    const int n0 = tn * kBN;
+
+    // per-lane 32-bit offsets of this wave's load slots from the tile bases
+    uint32_t aoff[AJ], boff[BJ];
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+        const int q = (j * 4 + wave) * 64 + lane;
+        const int row = q >> 2;
+        const int c = (q & 3) ^ ((row >> 2) & 3);
+        aoff[j] = (uint32_t)(min(m0 + row, M - 1) - m0) * (uint32_t)K + c * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+        const int q = (j * 4 + wave) * 64 + lane;
+        const int row = q >> 2;
+        const int c = (q & 3) ^ ((row >> 2) & 3);
+        boff[j] = (uint32_t)(min(n0 + row, N - 1) - n0) * (uint32_t)K + c * 16;
+    }
+    const int8_t* const abase = W + (size_t)m0 * K;
+    const int8_t* const bbase = x_q + (size_t)n0 * K;
+    // scale sources: thread tid covers weight row m0 + tid and token n0 + tid
+    const int srow = min(m0 + tid, M - 1);
+    const int stok = min(n0 + tid, N - 1);
+    const size_t sbase = G == 1 ? (size_t)srow : (size_t)srow * G;
+    const int G1 = G == 1 ? 0 : 1;
+
+    const int nsub = K >> 6;                 // 64-byte substeps
+    const int nstages = nsub / KS;
+    const int spg_m1 = (1 << lg_spg) - 1;
+
+    // Stage `stage`: its KS substeps of A/B tiles, plus the raw scales of the
+    // groups that start in stage + 1 (one per substep slot; unused slots
+    // carry a harmless duplicate so every wave issues the same loads).
+    auto issue = [&](int stage, int u) {
+        const int st = stage < nstages ? stage : nstages - 1;
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            const size_t koff = (size_t)(st * KS + q) * 64;
+#pragma unroll
+            for (int j = 0; j < AJ; ++j)
+                dma16_so(abase + koff, aoff[j], lds_addr(&As[u][q][(j * 4 + wave) * 1024]));
+#pragma unroll
+            for (int j = 0; j < BJ; ++j)
+                dma16_so(bbase + koff, boff[j], lds_addr(&Bs[u][q][(j * 4 + wave) * 1024]));
+            int gn = ((st + 1) * KS + q) >> lg_spg;
+            gn = gn < G ? gn : G - 1;
+            const size_t wi = sbase + (size_t)gn * G1;
+            dma4(w_scale + (wi & ~(size_t)1), lds_addr(&wsr[u][q][wave * 64]));
+            dma4(x_scale + (size_t)stok * G + gn, lds_addr(&xsr[u][q][wave * 64]));
+        }
+    };
+
+    // groups starting in stage 0, from plain loads; then the prologue
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+        if ((q & spg_m1) == 0) {
+            const int gi = q >> lg_spg;
+            if (tid < BM) ws_f[gi & 3][tid] = h2f(w_scale[sbase + (size_t)gi * G1]);
+            if (tid < kBN) xs_f[gi & 3][tid] = x_scale[(size_t)stok * G + gi];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kNst - 1; ++u) issue(u, u);
+
+    v16i P[RB][2];
+    float acc[RB][2][16];
+    v16i zero16;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) zero16[e] = 0;
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                P[i][j][e] = 0;
+                acc[i][j][e] = 0.0f;
+            }
+
+    const int fr = lane & 31;
+    const int fh = lane >> 5;
+    for (int s0 = 0; s0 < nstages; s0 += kNst) {
+#pragma unroll
+        for (int u = 0; u < kNst; ++u) {
+            const int s = s0 + u;
+            wait_vm<kYounger>();
+            __syncthreads();
+            // groups starting in stage s + 1: their raw scales came with stage s
+#pragma unroll
+            for (int q = 0; q < KS; ++q) {
+                const int tnext = (s + 1) * KS + q;
+                if ((tnext & spg_m1) == 0 && tnext < nsub) {
+                    const int gn = tnext >> lg_spg;
+                    if (tid < BM) {
+                        const uint32_t d = wsr[u][q][tid];
+                        const size_t wi = sbase + (size_t)gn * G1;
+                        ws_f[gn & 3][tid] = h2f((uint16_t)((wi & 1) ? (d >> 16) : (d & 0xffffu)));
+                    }
+                    if (tid < kBN) xs_f[gn & 3][tid] = xsr[u][q][tid];
+                }
+            }
+            issue(s + kNst - 1, (u + kNst - 1) % kNst);
+#pragma unroll
+            for (int q = 0; q < KS; ++q) {
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    v4i a[RB], bb[2];
+#pragma unroll
+                    for (int i = 0; i < RB; ++i) {
+                        const int row = wm * (BM / 2) + i * 32 + fr;
+                        const int c = (kk * 2 + fh) ^ ((row >> 2) & 3);
+                        a[i] = *reinterpret_cast<const v4i*>(&As[u][q][(row * 4 + c) * 16]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int row = wn * 64 + j * 32 + fr;
+                        const int c = (kk * 2 + fh) ^ ((row >> 2) & 3);
+                        bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][q][(row * 4 + c) * 16]);
+                    }
+                    // first MFMA of a K-group starts from zero
+                    const bool fresh = kk == 0 && (((s * KS + q) & spg_m1) == 0);
+                    if (fresh) {
+#pragma unroll
+                        for (int i = 0; i < RB; ++i)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], zero16,
+                                                                                0, 0, 0);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < RB; ++i)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], P[i][j],
+                                                                                0, 0, 0);
+                    }
+                }
+                const int tcur = s * KS + q;
+                if (((tcur + 1) & spg_m1) == 0) {
+                    const int gi = tcur >> lg_spg;
+                    const int sl = gi & 3;
+#pragma unroll
+                    for (int i = 0; i < RB; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const int tl = wn * 64 + j * 32 + fr;
+                            const float xs = xs_f[sl][tl];
+#pragma unroll
+                            for (int e = 0; e < 16; ++e) {
+                                const int rl =
+                                    wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                                acc[i][j][e] = __builtin_fmaf((float)P[i][j][e] * ws_f[sl][rl], xs,
+                                                              acc[i][j][e]);
+                                if constexpr (kDbg) {
+                                    const int row = m0 + rl, tok = n0 + tl;
+                                    if (row < M && tok < N && dbg.in(row, tok))
+                                        dbg.at(row, tok, gi, G) = P[i][j][e];
+                                }
+                            }
+                        }
+                }
+            }
+        }
+    }
+    wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
+
+    // fp16 out: each lane holds 4 consecutive rows of one token per (i, j, e/4)
+    const bool vec = (M & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int tok = n0 + wn * 64 + j * 32 + fr;
+            if (tok >= N) continue;
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * e4 + 4 * fh;
+                uint16_t h[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) h[r] = f2h(acc[i][j][e4 * 4 + r]);
+                uint16_t* dst = Y + (size_t)tok * M + row;
+                if (vec && row + 3 < M) {
+                    uint2 u;
+                    u.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+                    u.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+                    *reinterpret_cast<uint2*>(dst) = u;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (row + r < M) dst[r] = h[r];
+                }
+            }
+        }
+}
+
 // Any K, any group size, any alignment: one wave per (row, token); lanes
 // stride the group, the int32 partial is reduced exactly across the wave and
 // scaled in the reference order.  Used only for shapes the MFMA kernels do
@@ -248,6 +531,33 @@ hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x
     else
         hipLaunchKernelGGL((gemm_mfma_kernel<false>), grid, dim3(256), 0, stream, W, w_scale, x_q,
                            x_scale, Y, dbg, M, N, K, g, G, tiles_m);
+    return hipGetLastError();
+}
+
+bool gemm_pipe_ok(int M, int N, int K, int g) {
+    (void)M;
+    (void)N;
+    // g a power of two >= 64, K a whole number of 128-byte stages (>= 4)
+    return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 512 && g <= K;
+}
+
+hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                            const float* x_scale, uint16_t* Y, int32_t* dbg_partials, int dbg_row0,
+                            int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g,
+                            int G, hipStream_t stream) {
+    DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
+    int lg_spg = 0;
+    while ((64 << lg_spg) < g) ++lg_spg;
+    // 128 x 128 tiles, two workgroups per CU, 128-byte K stages, 2-deep ring
+    const int tm = ceil_div(M, 128);
+    const int tn = ceil_div(N, kBN);
+    const dim3 grid((unsigned)(tm * tn));
+    if (dbg_partials)
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, true>), grid, dim3(256), 0, stream, W,
+                           w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+    else
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, false>), grid, dim3(256), 0, stream, W,
+                           w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     return hipGetLastError();
 }
 
