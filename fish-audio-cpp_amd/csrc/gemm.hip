@@ -538,7 +538,7 @@ bool gemm_pipe_ok(int M, int N, int K, int g) {
     (void)M;
     (void)N;
     // g a power of two >= 64, K a whole number of 128-byte stages (>= 4)
-    return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 512 && g <= K;
+    return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 256 && g <= K;
 }
 
 hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
@@ -548,15 +548,15 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
     int lg_spg = 0;
     while ((64 << lg_spg) < g) ++lg_spg;
-    // 128 x 128 tiles, two workgroups per CU, 128-byte K stages, 2-deep ring
+    // 128 x 128 tiles, two workgroups per CU, 64-byte K stages, 2-deep ring
     const int tm = ceil_div(M, 128);
     const int tn = ceil_div(N, kBN);
     const dim3 grid((unsigned)(tm * tn));
     if (dbg_partials)
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, true>), grid, dim3(256), 0, stream, W,
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 1, 2, 2, true>), grid, dim3(256), 0, stream, W,
                            w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     else
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, false>), grid, dim3(256), 0, stream, W,
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 1, 2, 2, false>), grid, dim3(256), 0, stream, W,
                            w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     return hipGetLastError();
 }
