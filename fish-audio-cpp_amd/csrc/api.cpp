@@ -50,6 +50,8 @@ struct Workspace {
     size_t xq_bytes = 0;
     float* xs = nullptr;
     size_t xs_bytes = 0;
+    float* st = nullptr;        // group-major scale tables of the pipelined GEMM
+    size_t st_bytes = 0;
 };
 
 thread_local std::unordered_map<int, Workspace> g_ws;
@@ -90,8 +92,15 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
         }
     }
     if (aligned && fa::gemm_pipe_ok(M, N, K, g)) {
-        FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, Y, dbg, row0, rows, tok0, toks, M, N, K, g,
-                                    G, stream));
+        Workspace* ws = nullptr;
+        int rc = current_ws(&ws);
+        if (rc) return rc;
+        void* p = ws->st;
+        rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(M, N, G), stream);
+        ws->st = (float*)p;
+        if (rc) return rc;
+        FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks, M,
+                                    N, K, g, G, stream));
         return FA_OK;
     }
     if (aligned && K % 64 == 0 && g % 64 == 0) {
@@ -317,6 +326,10 @@ int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_siz
     rc = grow(&p, &ws->xs_bytes, (size_t)max_tokens * (size_t)G * sizeof(float), s);
     ws->xs = (float*)p;
     if (rc) return rc;
+    p = ws->st;
+    rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(max_M, max_tokens, G), s);
+    ws->st = (float*)p;
+    if (rc) return rc;
     return FA_OK;
 }
 
@@ -328,6 +341,7 @@ int fa_workspace_release(void) {
     FA_HIP(hipDeviceSynchronize());
     if (ws->xq) FA_HIP(hipFree(ws->xq));
     if (ws->xs) FA_HIP(hipFree(ws->xs));
+    if (ws->st) FA_HIP(hipFree(ws->st));
     *ws = Workspace{};
     return FA_OK;
 }

@@ -118,10 +118,13 @@ hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x
 // Prefill GEMM with a direct-to-LDS multi-stage pipeline (K % 256 == 0,
 // g % 64 == 0).
 bool gemm_pipe_ok(int M, int N, int K, int g);
+// Scratch the pipelined GEMM needs for its group-major scale tables.
+size_t gemm_pipe_tables_bytes(int M, int N, int G);
+// Two launches: the scale tables into `tables`, then the GEMM.
 hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
-                            const float* x_scale, uint16_t* Y, int32_t* dbg_partials, int dbg_row0,
-                            int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g,
-                            int G, hipStream_t stream);
+                            const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
+                            int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
+                            int K, int g, int G, hipStream_t stream);
 
 // Any-shape fallback (any K, any group size, unaligned pointers).
 hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,

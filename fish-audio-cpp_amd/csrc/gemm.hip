@@ -21,6 +21,8 @@
 //   the group's scales ride along with its first stage into LDS.
 #include "common.h"
 
+#include <algorithm>
+
 namespace fa {
 namespace {
 
@@ -205,6 +207,30 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(
         }
 }
 
+// Group-major scale tables for the pipelined kernel: wsT [G][M] (weight
+// scales widened to fp32, exact) and xsT [G][N].  With them the 128 scales of
+// one tile and group are one contiguous 512-byte run instead of 128 strided
+// words.
+__global__ __launch_bounds__(256) void scale_tables_kernel(const uint16_t* __restrict__ w_scale,
+                                                           const float* __restrict__ x_scale,
+                                                           float* __restrict__ wsT,
+                                                           float* __restrict__ xsT, int M, int N,
+                                                           int G) {
+    const size_t nw = (size_t)G * M;
+    const size_t total = nw + (size_t)G * N;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * 256) {
+        if (i < nw) {
+            const size_t gi = i / M, r = i % M;
+            wsT[i] = h2f(w_scale[G == 1 ? r : r * G + gi]);
+        } else {
+            const size_t j = i - nw;
+            const size_t gi = j / N, t = j % N;
+            xsT[j] = x_scale[t * G + gi];
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Pipelined kernel (K % 256 == 0): kNst-deep LDS ring filled by direct
 // global->LDS loads.
@@ -250,34 +276,48 @@ __device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint3
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                  :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
+// LDS swizzle of a stage row: 16 lanes of a ds_read_b128 (16 consecutive rows,
+// one logical chunk) land on 16 distinct 16-byte positions of the 256-byte
+// bank window (64-byte rows: 4 rows per window; 128-byte rows: 2).
+template <int KS>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (KS == 1) return (row >> 2) & 3;
+    else return (row >> 1) & 7;
+}
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
-template <int BM, int KS, int kNst, int kOcc, bool kDbg>
-__global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
-    const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
-    const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
+template <int BM, int KS, int kNst, int kOcc, bool kDbg, int kAb = 0>
+__global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ wsT,
+    const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int lg_spg, int G, int tiles_m,
     int tiles_n) {
-    constexpr int RB = BM / 64;              // 32-row blocks per wave
-    constexpr int AJ = BM / 64;              // A loads per wave per 64-byte substep
-    constexpr int BJ = kBN / 64;             // B loads per wave per substep
-    constexpr int kPerStage = KS * (AJ + BJ + 2);
+    static_assert(BM == 128 || BM == 256, "BM");
+    constexpr int NW = BM / 32;              // waves: (BM / 64) along M x 2 along N
+    constexpr int WMN = BM / 64;
+    constexpr int RB = 2;                    // wave tile 64 x 64 = 2 x 2 blocks of 32 x 32
+    constexpr int CPR = KS * 4;              // 16-byte chunks per row and stage
+    constexpr int AJ = BM * CPR / 64 / NW;   // A loads per wave per stage
+    constexpr int BJ = kBN * CPR / 64 / NW;  // B loads per wave per stage
+    static_assert(AJ * NW * 64 == BM * CPR && BJ * NW * 64 == kBN * CPR, "load split");
+    constexpr int kPerStage = AJ + BJ + KS;
     constexpr int kYounger = (kNst - 2) * kPerStage;
-    __shared__ __align__(16) int8_t As[kNst][KS][BM * 64];
-    __shared__ __align__(16) int8_t Bs[kNst][KS][kBN * 64];
-    __shared__ __align__(16) uint32_t wsr[kNst][KS][256];   // raw scale dwords
-    __shared__ __align__(16) float xsr[kNst][KS][256];
-    __shared__ __align__(16) float ws_f[4][BM];             // converted, ring by group & 3
-    __shared__ __align__(16) float xs_f[4][kBN];
+    // stage u holds KS * 64 bytes of K per row, rows contiguous; 16-byte
+    // chunk c of row r sits at physical chunk c ^ swz(r)
+    __shared__ __align__(16) int8_t As[kNst][BM * CPR * 16];
+    __shared__ __align__(16) int8_t Bs[kNst][kBN * CPR * 16];
+    // scales of one group: [0, BM) weight rows, [BM, BM + 128) tokens
+    __shared__ __align__(16) float sr[kNst][KS][BM + kBN];  // as fetched with a stage
+    __shared__ __align__(16) float sf[4][BM + kBN];         // ring by group & 3
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1;
-    const int wn = wave >> 1;
+    const int wm = wave % WMN;
+    const int wn = wave / WMN;
 
     const int ntiles = tiles_m * tiles_n;
     const int b = blockIdx.x;
@@ -292,49 +332,50 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
     uint32_t aoff[AJ], boff[BJ];
 #pragma unroll
     for (int j = 0; j < AJ; ++j) {
-        const int q = (j * 4 + wave) * 64 + lane;
-        const int row = q >> 2;
-        const int c = (q & 3) ^ ((row >> 2) & 3);
+        const int q = (j * NW + wave) * 64 + lane;
+        const int row = q / CPR;
+        const int c = (q % CPR) ^ swz<KS>(row);
         aoff[j] = (uint32_t)(min(m0 + row, M - 1) - m0) * (uint32_t)K + c * 16;
     }
 #pragma unroll
     for (int j = 0; j < BJ; ++j) {
-        const int q = (j * 4 + wave) * 64 + lane;
-        const int row = q >> 2;
-        const int c = (q & 3) ^ ((row >> 2) & 3);
+        const int q = (j * NW + wave) * 64 + lane;
+        const int row = q / CPR;
+        const int c = (q % CPR) ^ swz<KS>(row);
         boff[j] = (uint32_t)(min(n0 + row, N - 1) - n0) * (uint32_t)K + c * 16;
     }
     const int8_t* const abase = W + (size_t)m0 * K;
     const int8_t* const bbase = x_q + (size_t)n0 * K;
-    // scale sources: thread tid covers weight row m0 + tid and token n0 + tid
-    const int srow = min(m0 + tid, M - 1);
-    const int stok = min(n0 + tid, N - 1);
-    const size_t sbase = G == 1 ? (size_t)srow : (size_t)srow * G;
-    const int G1 = G == 1 ? 0 : 1;
+    // scale source of thread tid in the group-major tables wsT [G][M], xsT [G][N]:
+    // weight row m0 + tid, else token n0 + (tid - BM) % 128.  Waves past
+    // BM + 128 threads repeat the token fetch of the two waves before them,
+    // same data to the same LDS words, so every wave issues the same loads.
+    const int stk = (tid - BM) & (kBN - 1);
+    const int sslot = wave >= (BM + kBN) / 64 ? wave - 2 : wave;
+    const float* const ssrc = tid < BM ? wsT + min(m0 + tid, M - 1) : xsT + min(n0 + stk, N - 1);
+    const size_t sstride = tid < BM ? (size_t)M : (size_t)N;
 
     const int nsub = K >> 6;                 // 64-byte substeps
     const int nstages = nsub / KS;
     const int spg_m1 = (1 << lg_spg) - 1;
 
-    // Stage `stage`: its KS substeps of A/B tiles, plus the raw scales of the
-    // groups that start in stage + 1 (one per substep slot; unused slots
-    // carry a harmless duplicate so every wave issues the same loads).
+    // Stage `stage`: its A/B tiles plus the scales of the groups that start
+    // in stage + 1 (one slot per substep; unused slots fetch a duplicate).
     auto issue = [&](int stage, int u) {
+        if constexpr ((kAb & 8) != 0) return;
         const int st = stage < nstages ? stage : nstages - 1;
+        const size_t koff = (size_t)st * KS * 64;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j)
+            dma16_so(abase + koff, aoff[j], lds_addr(&As[u][(j * NW + wave) * 1024]));
+#pragma unroll
+        for (int j = 0; j < BJ; ++j)
+            dma16_so(bbase + koff, boff[j], lds_addr(&Bs[u][(j * NW + wave) * 1024]));
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
-            const size_t koff = (size_t)(st * KS + q) * 64;
-#pragma unroll
-            for (int j = 0; j < AJ; ++j)
-                dma16_so(abase + koff, aoff[j], lds_addr(&As[u][q][(j * 4 + wave) * 1024]));
-#pragma unroll
-            for (int j = 0; j < BJ; ++j)
-                dma16_so(bbase + koff, boff[j], lds_addr(&Bs[u][q][(j * 4 + wave) * 1024]));
             int gn = ((st + 1) * KS + q) >> lg_spg;
             gn = gn < G ? gn : G - 1;
-            const size_t wi = sbase + (size_t)gn * G1;
-            dma4(w_scale + (wi & ~(size_t)1), lds_addr(&wsr[u][q][wave * 64]));
-            dma4(x_scale + (size_t)stok * G + gn, lds_addr(&xsr[u][q][wave * 64]));
+            dma4(ssrc + (size_t)gn * sstride, lds_addr(&sr[u][q][sslot * 64]));
         }
     };
 
@@ -343,8 +384,7 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
     for (int q = 0; q < KS; ++q) {
         if ((q & spg_m1) == 0) {
             const int gi = q >> lg_spg;
-            if (tid < BM) ws_f[gi & 3][tid] = h2f(w_scale[sbase + (size_t)gi * G1]);
-            if (tid < kBN) xs_f[gi & 3][tid] = x_scale[(size_t)stok * G + gi];
+            if (tid < BM + kBN) sf[gi & 3][tid] = ssrc[(size_t)gi * sstride];
         }
     }
     __syncthreads();
@@ -372,21 +412,14 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
 #pragma unroll
         for (int u = 0; u < kNst; ++u) {
             const int s = s0 + u;
-            wait_vm<kYounger>();
+            if constexpr ((kAb & 8) == 0) wait_vm<kYounger>();
             __syncthreads();
-            // groups starting in stage s + 1: their raw scales came with stage s
+            // groups starting in stage s + 1: their scales came with stage s
 #pragma unroll
             for (int q = 0; q < KS; ++q) {
                 const int tnext = (s + 1) * KS + q;
-                if ((tnext & spg_m1) == 0 && tnext < nsub) {
-                    const int gn = tnext >> lg_spg;
-                    if (tid < BM) {
-                        const uint32_t d = wsr[u][q][tid];
-                        const size_t wi = sbase + (size_t)gn * G1;
-                        ws_f[gn & 3][tid] = h2f((uint16_t)((wi & 1) ? (d >> 16) : (d & 0xffffu)));
-                    }
-                    if (tid < kBN) xs_f[gn & 3][tid] = xsr[u][q][tid];
-                }
+                if ((tnext & spg_m1) == 0 && tnext < nsub && tid < BM + kBN)
+                    sf[(tnext >> lg_spg) & 3][tid] = sr[u][q][tid];
             }
             issue(s + kNst - 1, (u + kNst - 1) % kNst);
 #pragma unroll
@@ -396,19 +429,30 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
                     v4i a[RB], bb[2];
 #pragma unroll
                     for (int i = 0; i < RB; ++i) {
-                        const int row = wm * (BM / 2) + i * 32 + fr;
-                        const int c = (kk * 2 + fh) ^ ((row >> 2) & 3);
-                        a[i] = *reinterpret_cast<const v4i*>(&As[u][q][(row * 4 + c) * 16]);
+                        const int row = wm * 64 + i * 32 + fr;
+                        const int c = (q * 4 + kk * 2 + fh) ^ swz<KS>(row);
+                        if constexpr ((kAb & 2) == 0)
+                            a[i] = *reinterpret_cast<const v4i*>(&As[u][(row * CPR + c) * 16]);
+                        else
+                            a[i] = v4i{row, c, s, kk};
                     }
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int row = wn * 64 + j * 32 + fr;
-                        const int c = (kk * 2 + fh) ^ ((row >> 2) & 3);
-                        bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][q][(row * 4 + c) * 16]);
+                        const int c = (q * 4 + kk * 2 + fh) ^ swz<KS>(row);
+                        if constexpr ((kAb & 2) == 0)
+                            bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][(row * CPR + c) * 16]);
+                        else
+                            bb[j] = v4i{c, row, kk, s};
                     }
                     // first MFMA of a K-group starts from zero
                     const bool fresh = kk == 0 && (((s * KS + q) & spg_m1) == 0);
-                    if (fresh) {
+                    if constexpr ((kAb & 1) != 0) {
+#pragma unroll
+                        for (int i = 0; i < RB; ++i)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) P[i][j][0] ^= a[i].x ^ bb[j].y;
+                    } else if (fresh) {
 #pragma unroll
                         for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -425,7 +469,7 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
                     }
                 }
                 const int tcur = s * KS + q;
-                if (((tcur + 1) & spg_m1) == 0) {
+                if ((kAb & 4) == 0 && ((tcur + 1) & spg_m1) == 0) {
                     const int gi = tcur >> lg_spg;
                     const int sl = gi & 3;
 #pragma unroll
@@ -433,12 +477,11 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
 #pragma unroll
                         for (int j = 0; j < 2; ++j) {
                             const int tl = wn * 64 + j * 32 + fr;
-                            const float xs = xs_f[sl][tl];
+                            const float xs = sf[sl][BM + tl];
 #pragma unroll
                             for (int e = 0; e < 16; ++e) {
-                                const int rl =
-                                    wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
-                                acc[i][j][e] = __builtin_fmaf((float)P[i][j][e] * ws_f[sl][rl], xs,
+                                const int rl = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                                acc[i][j][e] = __builtin_fmaf((float)P[i][j][e] * sf[sl][rl], xs,
                                                               acc[i][j][e]);
                                 if constexpr (kDbg) {
                                     const int row = m0 + rl, tok = n0 + tl;
@@ -452,6 +495,14 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
         }
     }
     wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
+    if constexpr ((kAb & 4) != 0) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] += (float)P[i][j][e];
+    }
 
     // fp16 out: each lane holds 4 consecutive rows of one token per (i, j, e/4)
     const bool vec = (M & 3) == 0;
@@ -463,7 +514,7 @@ __global__ __launch_bounds__(256, kOcc) void gemm_pipe_kernel(
             if (tok >= N) continue;
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {
-                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * e4 + 4 * fh;
+                const int row = m0 + wm * 64 + i * 32 + 8 * e4 + 4 * fh;
                 uint16_t h[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) h[r] = f2h(acc[i][j][e4 * 4 + r]);
@@ -541,23 +592,33 @@ bool gemm_pipe_ok(int M, int N, int K, int g) {
     return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 256 && g <= K;
 }
 
+size_t gemm_pipe_tables_bytes(int M, int N, int G) {
+    return (size_t)G * ((size_t)M + (size_t)N) * sizeof(float);
+}
+
 hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
-                            const float* x_scale, uint16_t* Y, int32_t* dbg_partials, int dbg_row0,
-                            int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N, int K, int g,
-                            int G, hipStream_t stream) {
+                            const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
+                            int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
+                            int K, int g, int G, hipStream_t stream) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
     int lg_spg = 0;
     while ((64 << lg_spg) < g) ++lg_spg;
-    // 128 x 128 tiles, two workgroups per CU, 64-byte K stages, 2-deep ring
+    float* const wsT = tables;
+    float* const xsT = tables + (size_t)G * M;
+    const size_t total = (size_t)G * ((size_t)M + (size_t)N);
+    const unsigned pblocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(scale_tables_kernel, dim3(pblocks), dim3(256), 0, stream, w_scale, x_scale,
+                       wsT, xsT, M, N, G);
+    // 128 x 128 tiles, two workgroups per CU, 128-byte K stages, 2-deep ring
     const int tm = ceil_div(M, 128);
     const int tn = ceil_div(N, kBN);
     const dim3 grid((unsigned)(tm * tn));
     if (dbg_partials)
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 1, 2, 2, true>), grid, dim3(256), 0, stream, W,
-                           w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, true>), grid, dim3(256), 0, stream, W,
+                           wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     else
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 1, 2, 2, false>), grid, dim3(256), 0, stream, W,
-                           w_scale, x_q, x_scale, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, false>), grid, dim3(256), 0, stream, W,
+                           wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     return hipGetLastError();
 }
 

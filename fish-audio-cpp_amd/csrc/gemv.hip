@@ -69,6 +69,16 @@ __device__ __forceinline__ int group_sum(int p, int lg_rt) {
     }
 }
 
+// One wave streams R rows (R = 1, 2 or 4; 64/R lanes per row, 16 bytes per
+// lane per pass).  After 4 v_dot4 per lane, lanes of one K-group (LG = g/16
+// of them) sum their partials with DPP, so every lane of a group holds the
+// exact int32 P_g.  The groups of a pass are then in known lanes: group slot j
+// of row r sits in lane r * 64/R + j * LG.  Each of those terms
+// float(P_g) * ws is broadcast with v_readlane, and every lane advances its
+// rows' fp32 sums in group order, acc = fma(term, x_scale[g], acc) -- the
+// reference's accumulate order (int8_gemm.cu:231), so the result is the
+// oracle's bit for bit without any per-row serial tail.
+//
 // QX: the kernel quantizes the fp16 token itself (int8_gemm.cu:147-211
 // semantics: per-group amax/127 or a static scale, optional smooth_inv) while
 // the first weight loads are in flight; otherwise it stages the given int8
@@ -76,9 +86,9 @@ __device__ __forceinline__ int group_sum(int p, int lg_rt) {
 //
 // Work: row blocks of kDotWaves * R rows; block b, b + gridDim.x, ... belong to
 // workgroup b.  A uniform cursor (row block, pass) walks the wave's passes in
-// order; the weight ring is KD passes ahead of the consumer.  g is a power of
-// two (lg_g = log2 g), so group indices are shifts.
-template <int R, int KD, int LG, bool QX, int XV>
+// order and the weight ring is KD passes ahead of the consumer.  g is a power
+// of two (lg_g = log2 g) with 16 <= g <= 16 * 64/R.
+template <int R, int KD, int LG, bool QX, int XV, int kAb = 0>
 __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
@@ -88,28 +98,28 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     int nblocks) {
     constexpr int RL = 64 / R;            // lanes per row
     constexpr int PB = RL * 16;           // bytes of a row per pass
+    constexpr int GPP = RL / LG;          // groups per row per pass
     constexpr int NT = kDotWaves * 64;
+    static_assert(LG >= 1 && LG <= RL, "group must fit a row's lanes");
     extern __shared__ __align__(16) float lds[];
     const int Kp = (K + 15) & ~15;
     int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                  // [Kp]
     float* xs_s = lds + Kp / 4;                                      // [G]
+    int* gmax = reinterpret_cast<int*>(xs_s + G);                    // [G] (QX)
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    float* terms = xs_s + G + wave * R * G;                          // [R][G]
-    int* gmax = reinterpret_cast<int*>(xs_s + G + kDotWaves * R * G);  // [G] (QX)
 
     const int rsub = lane / RL;
     const int li = lane % RL;
     const int lane_k = li * 16;
-    const bool leader = (li & ((LG ? LG : 1) - 1)) == 0;
 
     // ---- activation loads first: their wait then does not cover the ring.
-    // XV 16-byte chunks per thread (int8 codes, or 8 fp16 values with QX).
+    // XV 16-byte chunks per thread (int8 codes, or 8 fp16 values with QX);
+    // unconditional loads from clamped addresses (a load under a branch makes
+    // the compiler wait for it on the spot).
     v4i xr[XV];
     float xsr = 0.0f;
-    // (unconditional loads from clamped addresses: a load under a branch makes
-    // the compiler wait for it on the spot)
     if constexpr (!QX) {
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
@@ -135,13 +145,16 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     auto load = [&](int slot) {
         const bool live = l_blk < nblocks;
         const int row = row_of_blk(live ? l_blk : blockIdx.x);
+        const int rowc = row < M ? row : M - 1;
         const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
         const int k = l_pass * PB + lane_k;
         const bool ok = live && k < K;
         const int kk = ok ? k : 0;
         const v4i wa = ld16(wrow + kk);
-        sc[slot] = w_scale[G == 1 ? (size_t)(row < M ? row : M - 1)
-                                  : (size_t)(row < M ? row : M - 1) * G + (kk >> lg_g)];
+        if constexpr ((kAb & 2) == 0)
+            sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
+        else
+            sc[slot] = (uint16_t)kk;
         a[slot] = ok ? wa : zero;
         if (++l_pass == passes) {
             l_pass = 0;
@@ -152,7 +165,8 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     for (int s = 0; s < KD; ++s) load(s);
 
     // ---- stage activations into LDS
-    if constexpr (!QX) {
+    if constexpr ((kAb & 1) != 0) {
+    } else if constexpr (!QX) {
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
             const int k = (tid + i * NT) * 16;
@@ -225,40 +239,51 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
         for (int k = (tid + XV * NT) * 8; k < K; k += NT * 8)
             quant_chunk(k, *reinterpret_cast<const v4i*>(X + k));
     }
-    __syncthreads();
+    if constexpr ((kAb & 1) == 0) __syncthreads();
 
-    // ---- consume: per pass 4 v_dot4, a lane-group sum, one term per group
+    // ---- consume
     int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     auto consume = [&](int slot) {
-        const int k = c_pass * PB + lane_k;
-        const v4i b = *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
+        const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
+        const int k = kbase + lane_k;
+        const v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
         int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
         p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
         p = __builtin_amdgcn_sdot4(a[slot].z, b.z, p, false);
         p = __builtin_amdgcn_sdot4(a[slot].w, b.w, p, false);
-        p = group_sum<LG>(p, lg_g - 4);
-        const int row = row_of_blk(c_blk);
-        const bool lead = LG ? leader : (li & ((1 << (lg_g - 4)) - 1)) == 0;
-        if (k < K && lead) {
-            const int gi = k >> lg_g;
-            terms[rsub * G + gi] = (float)p * h2f(sc[slot]);
-            if (dbg.p && row < M && dbg.in(row, 0)) dbg.at(row, 0, gi, G) = p;
+        p = group_sum<LG>(p, 0);
+        const float term = (float)p * h2f(sc[slot]);
+        if (dbg.p) {
+            const int row = row_of_blk(c_blk);
+            if (k < K && (li & (LG - 1)) == 0 && row < M && dbg.in(row, 0))
+                dbg.at(row, 0, k >> lg_g, G) = p;
+        }
+        // group order within the pass: slot j of every row
+#pragma unroll
+        for (int j = 0; j < GPP; ++j) {
+            const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
+            if (kg < K) {
+                const float xs = xs_s[kg >> lg_g];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float tj = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
+                                                         r * RL + j * LG));
+                    acc[r] = __builtin_fmaf(tj, xs, acc[r]);
+                }
+            }
         }
         if (++c_pass == passes) {
-            // Row done: the group-ordered fp32 chain on one lane per row.
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (li == 0 && row < M) {
-                float acc = 0.0f;
-                const float* t = terms + rsub * G;
-#pragma unroll 8
-                for (int gi = 0; gi < G; ++gi) acc = __builtin_fmaf(t[gi], xs_s[gi], acc);
-                Y[row] = f2h(acc);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int row = row_of_blk(c_blk);
+            // lane r*RL (li == 0) of row slot r stores that row
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (rsub == r && li == 0 && row < M) Y[row] = f2h(acc[r]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
             c_pass = 0;
             c_blk += gridDim.x;
         }
@@ -385,9 +410,10 @@ using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const floa
 template <int R, int KD, bool QX, int XV>
 DotFn dot_for_lg(int lg) {
     switch (lg) {
-        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV>;
-        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV>;
-        default: return gemv_dot_kernel<R, KD, 0, QX, XV>;
+        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV>;     // g64
+        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV>;     // g128
+        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV>;    // g256
+        default: return gemv_dot_kernel<R, KD, 32, QX, XV>;   // g512
     }
 }
 
@@ -450,8 +476,7 @@ int round_maxg(int m) {
 
 GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
     GemvPlan p{};
-    const bool pow2_lanes = g % 16 == 0 && ((g / 16) & (g / 16 - 1)) == 0;
-    if (N == 1 && pow2_lanes && K % 16 == 0 && K <= 32768) {
+    if (N == 1 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 16 == 0 && K <= 32768) {
         const int lgroups = g / 16;
         p.kind = (M >= 4096 && lgroups <= 32) ? 2 : 1;   // rows per wave
         const int R = p.kind;
@@ -460,17 +485,13 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
         const int passes = (K + PB - 1) / PB;
         // ring depth: every pass of a row in flight when it fits (items flow
         // on into the next row either way)
-        static const int opts[] = {3, 4, 5, 8, 10};
-        p.kd = 10;
-        for (int o : opts)
-            if (o >= passes) {
-                p.kd = o;
-                break;
-            }
+        // ring depth: all passes of a row when they are few, else 5 (deeper
+        // rings cost more occupancy than they gain, measured on MI355X)
+        p.kd = passes <= 3 ? 3 : passes <= 4 ? 4 : 5;
         p.grid = ceil_div(M, kDotWaves * R);    // row blocks; capped at launch
         p.block = kDotWaves * 64;
         const int Kp = (K + 15) & ~15;
-        p.lds = (size_t)Kp + (size_t)(2 * G + kDotWaves * R * G) * sizeof(float);
+        p.lds = (size_t)Kp + (size_t)(2 * G) * sizeof(float);
         if (g < 16) return GemvPlan{};
         if (p.lds > 64 * 1024) return GemvPlan{};
         int lg = 0;
@@ -520,11 +541,8 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)
         DotFn fn = p.kind == 1 ? dot_for<1>(qx, K, p.kd, lgl) : dot_for<2>(qx, K, p.kd, lgl);
-        // as many workgroups as fit at once, each with the same number of
-        // row blocks (no straggler round)
-        const int cap = dot_resident_blocks(fn, p.lds);
-        const int per_wg = ceil_div(p.grid, cap);
-        const int grid = ceil_div(p.grid, per_wg);
+        // one workgroup per row block (the cursor also serves a smaller grid)
+        const int grid = p.grid;
         hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,
                            X, act_scale, smooth_inv, Y, dbg, M, K, p.lg, G, p.passes, p.grid);
     } else if (p.kind == 3) {
