@@ -255,8 +255,6 @@ __global__ __launch_bounds__(256) void scale_tables_kernel(const uint16_t* __res
 // Workgroups are dealt round-robin over the 8 XCDs; tile t is mapped so each
 // XCD runs a contiguous, row-block-major run of tiles and a weight-row block
 // is fetched into one XCD's L2 and reused by all of its token tiles.
-constexpr int kBN = 128;
-
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
 }
@@ -289,29 +287,32 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
-template <int BM, int KS, int kNst, int kOcc, bool kDbg, int kAb = 0>
+template <int BM, int BN, int KS, int kNst, int kOcc, bool kDbg, int kAb = 0>
 __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ wsT,
     const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int lg_spg, int G, int tiles_m,
     int tiles_n) {
     static_assert(BM == 128 || BM == 256, "BM");
+    static_assert(BN == 64 || BN == 128, "BN");
     constexpr int NW = BM / 32;              // waves: (BM / 64) along M x 2 along N
     constexpr int WMN = BM / 64;
-    constexpr int RB = 2;                    // wave tile 64 x 64 = 2 x 2 blocks of 32 x 32
+    constexpr int RB = 2;                    // wave tile 64 x (BN / 2): RB x JB blocks of 32 x 32
+    constexpr int JB = BN / 64;
+    constexpr int WC = BN / 2;               // tokens per wave
     constexpr int CPR = KS * 4;              // 16-byte chunks per row and stage
     constexpr int AJ = BM * CPR / 64 / NW;   // A loads per wave per stage
-    constexpr int BJ = kBN * CPR / 64 / NW;  // B loads per wave per stage
-    static_assert(AJ * NW * 64 == BM * CPR && BJ * NW * 64 == kBN * CPR, "load split");
+    constexpr int BJ = BN * CPR / 64 / NW;  // B loads per wave per stage
+    static_assert(AJ * NW * 64 == BM * CPR && BJ * NW * 64 == BN * CPR, "load split");
     constexpr int kPerStage = AJ + BJ + KS;
     constexpr int kYounger = (kNst - 2) * kPerStage;
     // stage u holds KS * 64 bytes of K per row, rows contiguous; 16-byte
     // chunk c of row r sits at physical chunk c ^ swz(r)
     __shared__ __align__(16) int8_t As[kNst][BM * CPR * 16];
-    __shared__ __align__(16) int8_t Bs[kNst][kBN * CPR * 16];
+    __shared__ __align__(16) int8_t Bs[kNst][BN * CPR * 16];
     // scales of one group: [0, BM) weight rows, [BM, BM + 128) tokens
-    __shared__ __align__(16) float sr[kNst][KS][BM + kBN];  // as fetched with a stage
-    __shared__ __align__(16) float sf[4][BM + kBN];         // ring by group & 3
+    __shared__ __align__(16) float sr[kNst][KS][BM + BN];  // as fetched with a stage
+    __shared__ __align__(16) float sf[4][BM + BN];         // ring by group & 3
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     const int tm = t / tiles_n;
     const int tn = t % tiles_n;
     const int m0 = tm * BM;
-    const int n0 = tn * kBN;
+    const int n0 = tn * BN;
 
     // per-lane 32-bit offsets of this wave's load slots from the tile bases
     uint32_t aoff[AJ], boff[BJ];
@@ -347,11 +348,11 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     const int8_t* const abase = W + (size_t)m0 * K;
     const int8_t* const bbase = x_q + (size_t)n0 * K;
     // scale source of thread tid in the group-major tables wsT [G][M], xsT [G][N]:
-    // weight row m0 + tid, else token n0 + (tid - BM) % 128.  Waves past
-    // BM + 128 threads repeat the token fetch of the two waves before them,
-    // same data to the same LDS words, so every wave issues the same loads.
-    const int stk = (tid - BM) & (kBN - 1);
-    const int sslot = wave >= (BM + kBN) / 64 ? wave - 2 : wave;
+    // weight row m0 + tid, else token n0 + (tid - BM) % BN.  Waves past
+    // BM + BN threads repeat the token fetch of the waves before them, same
+    // data to the same LDS words, so every wave issues the same loads.
+    const int stk = (tid - BM) & (BN - 1);
+    const int sslot = wave >= (BM + BN) / 64 ? BM / 64 + (wave - BM / 64) % (BN / 64) : wave;
     const float* const ssrc = tid < BM ? wsT + min(m0 + tid, M - 1) : xsT + min(n0 + stk, N - 1);
     const size_t sstride = tid < BM ? (size_t)M : (size_t)N;
 
@@ -384,22 +385,22 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     for (int q = 0; q < KS; ++q) {
         if ((q & spg_m1) == 0) {
             const int gi = q >> lg_spg;
-            if (tid < BM + kBN) sf[gi & 3][tid] = ssrc[(size_t)gi * sstride];
+            if (tid < BM + BN) sf[gi & 3][tid] = ssrc[(size_t)gi * sstride];
         }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kNst - 1; ++u) issue(u, u);
 
-    v16i P[RB][2];
-    float acc[RB][2][16];
+    v16i P[RB][JB];
+    float acc[RB][JB][16];
     v16i zero16;
 #pragma unroll
     for (int e = 0; e < 16; ++e) zero16[e] = 0;
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < JB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 P[i][j][e] = 0;
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
             for (int q = 0; q < KS; ++q) {
                 const int tnext = (s + 1) * KS + q;
-                if ((tnext & spg_m1) == 0 && tnext < nsub && tid < BM + kBN)
+                if ((tnext & spg_m1) == 0 && tnext < nsub && tid < BM + BN)
                     sf[(tnext >> lg_spg) & 3][tid] = sr[u][q][tid];
             }
             issue(s + kNst - 1, (u + kNst - 1) % kNst);
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
             for (int q = 0; q < KS; ++q) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    v4i a[RB], bb[2];
+                    v4i a[RB], bb[JB];
 #pragma unroll
                     for (int i = 0; i < RB; ++i) {
                         const int row = wm * 64 + i * 32 + fr;
@@ -437,8 +438,8 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
                             a[i] = v4i{row, c, s, kk};
                     }
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int row = wn * 64 + j * 32 + fr;
+                    for (int j = 0; j < JB; ++j) {
+                        const int row = wn * WC + j * 32 + fr;
                         const int c = (q * 4 + kk * 2 + fh) ^ swz<KS>(row);
                         if constexpr ((kAb & 2) == 0)
                             bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][(row * CPR + c) * 16]);
@@ -451,19 +452,19 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
                         for (int i = 0; i < RB; ++i)
 #pragma unroll
-                            for (int j = 0; j < 2; ++j) P[i][j][0] ^= a[i].x ^ bb[j].y;
+                            for (int j = 0; j < JB; ++j) P[i][j][0] ^= a[i].x ^ bb[j].y;
                     } else if (fresh) {
 #pragma unroll
                         for (int i = 0; i < RB; ++i)
 #pragma unroll
-                            for (int j = 0; j < 2; ++j)
+                            for (int j = 0; j < JB; ++j)
                                 P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], zero16,
                                                                                 0, 0, 0);
                     } else {
 #pragma unroll
                         for (int i = 0; i < RB; ++i)
 #pragma unroll
-                            for (int j = 0; j < 2; ++j)
+                            for (int j = 0; j < JB; ++j)
                                 P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], P[i][j],
                                                                                 0, 0, 0);
                     }
@@ -475,8 +476,8 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
                     for (int i = 0; i < RB; ++i)
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            const int tl = wn * 64 + j * 32 + fr;
+                        for (int j = 0; j < JB; ++j) {
+                            const int tl = wn * WC + j * 32 + fr;
                             const float xs = sf[sl][BM + tl];
 #pragma unroll
                             for (int e = 0; e < 16; ++e) {
@@ -499,7 +500,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
         for (int i = 0; i < RB; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < JB; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] += (float)P[i][j][e];
     }
@@ -509,8 +510,8 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int tok = n0 + wn * 64 + j * 32 + fr;
+        for (int j = 0; j < JB; ++j) {
+            const int tok = n0 + wn * WC + j * 32 + fr;
             if (tok >= N) continue;
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {
@@ -609,16 +610,28 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
     const unsigned pblocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL(scale_tables_kernel, dim3(pblocks), dim3(256), 0, stream, w_scale, x_scale,
                        wsT, xsT, M, N, G);
-    // 128 x 128 tiles, two workgroups per CU, 128-byte K stages, 2-deep ring
+    // 128 x BN tiles, 128-byte K stages, 2-deep ring, two workgroups per CU.
+    // BN = 64 when 128-token tiles would number fewer than the 256 CUs.
     const int tm = ceil_div(M, 128);
-    const int tn = ceil_div(N, kBN);
+    const bool narrow = (size_t)tm * ceil_div(N, 128) < 256;
+    const int bn = narrow ? 64 : 128;
+    const int tn = ceil_div(N, bn);
     const dim3 grid((unsigned)(tm * tn));
-    if (dbg_partials)
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, true>), grid, dim3(256), 0, stream, W,
-                           wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
-    else
-        hipLaunchKernelGGL((gemm_pipe_kernel<128, 2, 2, 2, false>), grid, dim3(256), 0, stream, W,
-                           wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+    if (narrow) {
+        if (dbg_partials)
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 64, 2, 2, 2, true>), grid, dim3(256), 0, stream,
+                               W, wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+        else
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 64, 2, 2, 2, false>), grid, dim3(256), 0,
+                               stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+    } else {
+        if (dbg_partials)
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, 2, 2, true>), grid, dim3(256), 0,
+                               stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+        else
+            hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, 2, 2, false>), grid, dim3(256), 0,
+                               stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
+    }
     return hipGetLastError();
 }
 

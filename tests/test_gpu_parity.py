@@ -211,18 +211,19 @@ def test_config3_prefill_m512_qkv_bitexact():
     check_linear(512, Nout, K, 256, seed=6, full_entry=False)
 
 
+@pytest.mark.parametrize("N,g", [(512, 256), (2048, 256), (2048, 64)])
 @pytest.mark.parametrize("name", list(LAYER))
-def test_config3_prefill_m2048_g256_subblock(name):
-    """configs[3] at M=2048: int32 per-group partials bit-exact on a 64x64
-    output sub-block, fp16 outputs bit-exact on sampled rows x tokens."""
+def test_config3_prefill_subblock(name, N, g):
+    """configs[3] at M=512 and M=2048 (plus g64): int32 per-group partials
+    bit-exact on a 64x64 output sub-block, fp16 outputs bit-exact on sampled
+    rows x tokens.  M=512 runs the 64-token tiles for qkv, o and down."""
     K, Nout = LAYER[name]
-    N, g = 2048, 256
     torch.manual_seed(0)
     w = (torch.randn(Nout, K, device="cuda") * 0.02).half()
     Wd, Sd = ops.quantize_weights_groupwise(w, g)
     x = (torch.randn(N, K, device="cuda")).half()
     xq, xs = ops.quantize_activations(x, g)
-    r0, t0 = (Nout // 3) // 16 * 16 + 5, 1000 + 3
+    r0, t0 = (Nout // 3) // 16 * 16 + 5, N // 2 - 21
     Y, P = ops.w8a8_gemm_partials(Wd, Sd, g, xq, xs, row0=r0, rows=64, tok0=t0, toks=64)
     q, s, hq, hs, hY, hP = (host(t) for t in (Wd, Sd, xq, xs, Y, P))
     rP = ref.group_partials(q[r0:r0 + 64], hq[t0:t0 + 64], g)
