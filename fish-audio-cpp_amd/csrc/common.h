@@ -86,8 +86,9 @@ hipError_t launch_quantize_weights(const uint16_t* w, int64_t rows, int64_t K, i
 // kernel for 2 <= N <= 16.  kind == 0 means "shape not taken".
 struct GemvPlan {
     int kind = 0;    // 1, 2: dot kernel with 1 or 2 rows per wave; 3: MFMA kernel
-                     // (dot: grid = row blocks, capped at launch to the resident count)
+                     // (dot: grid = row blocks)
     int kd = 0;      // dot: passes in flight per wave
+    int split = 1;   // dot: waves sharing one row (1 or 2)
     int lg = 0;      // dot: log2(group size)
     int passes = 0;  // dot: passes per row
     int spg = 0;     // mfma: 64-byte K steps per group

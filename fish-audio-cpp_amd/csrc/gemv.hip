@@ -84,11 +84,18 @@ __device__ __forceinline__ int group_sum(int p, int lg_rt) {
 // the first weight loads are in flight; otherwise it stages the given int8
 // activations and fp32 scales.  Either way x_q [K] and x_scale [G] sit in LDS.
 //
-// Work: row blocks of kDotWaves * R rows; block b, b + gridDim.x, ... belong to
-// workgroup b.  A uniform cursor (row block, pass) walks the wave's passes in
-// order and the weight ring is KD passes ahead of the consumer.  g is a power
-// of two (lg_g = log2 g) with 16 <= g <= 16 * 64/R.
-template <int R, int KD, int LG, bool QX, int XV, int kAb = 0>
+// Work: row blocks of (kDotWaves / S) * R rows; block b, b + gridDim.x, ...
+// belong to workgroup b.  A uniform cursor (row block, pass) walks the wave's
+// passes in order and the weight ring is KD passes ahead of the consumer.  g is
+// a power of two (lg_g = log2 g) with 16 <= g <= 16 * 64/R.
+//
+// S = 2 splits every row's passes over a pair of waves (more, shorter streams
+// for long rows).  Both waves then leave their terms float(P_g) * ws in LDS
+// (double-buffered by row block); after a barrier at the end of the row block
+// the first wave runs the fp32 chain over all G groups in order, four terms
+// and scales per LDS read.  Both waves run the same number of passes (the
+// second may end with empty ones), so every wave meets the same barriers.
+template <int R, int KD, int LG, bool QX, int XV, int S = 1, int kAb = 0>
 __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
@@ -100,7 +107,9 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     constexpr int PB = RL * 16;           // bytes of a row per pass
     constexpr int GPP = RL / LG;          // groups per row per pass
     constexpr int NT = kDotWaves * 64;
+    constexpr int RS = kDotWaves / S;     // row slots per block
     static_assert(LG >= 1 && LG <= RL, "group must fit a row's lanes");
+    static_assert(S == 1 || S == 2, "split");
     extern __shared__ __align__(16) float lds[];
     const int Kp = (K + 15) & ~15;
     int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                  // [Kp]
@@ -109,6 +118,14 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
+    const int half = S == 2 ? (wave & 1) : 0;
+    const int wslot = S == 2 ? (wave >> 1) : wave;
+    const int PH = S == 2 ? (passes + 1) >> 1 : passes;              // passes per wave and row
+    const int pbase = half * PH;
+    // S == 2: terms of every group in LDS, [2][RS * R][TG], chained at row end
+    constexpr bool DEF = S == 2;
+    const int TG = (G + 3) & ~3;                                      // term slots per row
+    float* terms = lds + ((Kp / 4 + 2 * G + 3) & ~3);                // 16-byte aligned
 
     const int rsub = lane / RL;
     const int li = lane % RL;
@@ -141,22 +158,24 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     v4i a[KD];
     uint16_t sc[KD];
     const v4i zero = {0, 0, 0, 0};
-    auto row_of_blk = [&](int blk) { return (blk * kDotWaves + wave) * R + rsub; };
+    auto row_of_blk = [&](int blk) { return (blk * RS + wslot) * R + rsub; };
     auto load = [&](int slot) {
         const bool live = l_blk < nblocks;
         const int row = row_of_blk(live ? l_blk : blockIdx.x);
         const int rowc = row < M ? row : M - 1;
         const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
-        const int k = l_pass * PB + lane_k;
+        const int k = (pbase + l_pass) * PB + lane_k;
         const bool ok = live && k < K;
         const int kk = ok ? k : 0;
+        // no select on the loaded value (that would wait for the load here):
+        // bytes past K meet zero activations in consume()
         const v4i wa = ld16(wrow + kk);
         if constexpr ((kAb & 2) == 0)
             sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
         else
             sc[slot] = (uint16_t)kk;
-        a[slot] = ok ? wa : zero;
-        if (++l_pass == passes) {
+        a[slot] = wa;
+        if (++l_pass == PH) {
             l_pass = 0;
             l_blk += gridDim.x;
         }
@@ -243,13 +262,15 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
 
     // ---- consume
     int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
+    int tbuf = 0;                           // terms buffer of the current row block
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     auto consume = [&](int slot) {
-        const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
+        const int kbase = (pbase + c_pass) * PB;       // row offset of this pass (uniform)
         const int k = kbase + lane_k;
-        const v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
+        v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
+        if (k >= K) b = zero;
         int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
         p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
         p = __builtin_amdgcn_sdot4(a[slot].z, b.z, p, false);
@@ -261,27 +282,66 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
             if (k < K && (li & (LG - 1)) == 0 && row < M && dbg.in(row, 0))
                 dbg.at(row, 0, k >> lg_g, G) = p;
         }
-        // group order within the pass: slot j of every row
+        if constexpr ((kAb & 4) != 0) {
+            acc[0] += term;
+        } else if constexpr (DEF) {
+            if ((li & (LG - 1)) == 0 && k < K)
+                terms[(tbuf * RS * R + wslot * R + rsub) * TG + (k >> lg_g)] = term;
+        } else {
+            // group order within the pass: slot j of every row; the pass's
+            // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
+            float xsv[GPP];
+            const float* xp = xs_s + (kbase >> lg_g);
+            if constexpr (GPP == 4) {
+                const float4 v = *reinterpret_cast<const float4*>(xp);
+                xsv[0] = v.x; xsv[1] = v.y; xsv[2] = v.z; xsv[3] = v.w;
+            } else if constexpr (GPP == 2) {
+                const float2 v = *reinterpret_cast<const float2*>(xp);
+                xsv[0] = v.x; xsv[1] = v.y;
+            } else {
 #pragma unroll
-        for (int j = 0; j < GPP; ++j) {
-            const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
-            if (kg < K) {
-                const float xs = xs_s[kg >> lg_g];
+                for (int j = 0; j < GPP; ++j) xsv[j] = xp[j];
+            }
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float tj = __builtin_bit_cast(
-                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
-                                                         r * RL + j * LG));
-                    acc[r] = __builtin_fmaf(tj, xs, acc[r]);
+            for (int j = 0; j < GPP; ++j) {
+                const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
+                if (kg < K) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const float tj = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
+                                                             r * RL + j * LG));
+                        acc[r] = __builtin_fmaf(tj, xsv[j], acc[r]);
+                    }
                 }
             }
         }
-        if (++c_pass == passes) {
+        if (++c_pass == PH) {
             const int row = row_of_blk(c_blk);
+            if constexpr (DEF) {
+                if constexpr (S == 2) __syncthreads();
+                if (half == 0) {
+                    // every group in order, four terms and scales per LDS read
+                    const float* t = terms + (size_t)(tbuf * RS * R + wslot * R) * TG;
+                    for (int g4 = 0; g4 < G; g4 += 4) {
+                        const float4 xv = *reinterpret_cast<const float4*>(xs_s + g4);
+                        const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const float4 tv = *reinterpret_cast<const float4*>(t + r * TG + g4);
+                            const float te[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (g4 + e < G) acc[r] = __builtin_fmaf(te[e], xe[e], acc[r]);
+                        }
+                    }
+                }
+                if constexpr (S == 2) tbuf ^= 1;
+            }
             // lane r*RL (li == 0) of row slot r stores that row
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (rsub == r && li == 0 && row < M) Y[row] = f2h(acc[r]);
+                if (rsub == r && li == 0 && half == 0 && row < M) Y[row] = f2h(acc[r]);
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = 0.0f;
             c_pass = 0;
@@ -291,7 +351,7 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     // Rounds that refill the ring, then a last round that only drains it (so
     // every load is unconditional and the wait counts stay exact).
     const int my_blocks = (nblocks - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-    const int items = my_blocks * passes;
+    const int items = my_blocks * PH;
     int base = 0;
     for (; base + KD < items; base += KD) {
 #pragma unroll
@@ -407,33 +467,32 @@ using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const floa
                        const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,
                        int, int, int, int, int, int);
 
-template <int R, int KD, bool QX, int XV>
+template <int R, int S, int KD, bool QX, int XV>
 DotFn dot_for_lg(int lg) {
     switch (lg) {
-        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV>;     // g64
-        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV>;     // g128
-        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV>;    // g256
-        default: return gemv_dot_kernel<R, KD, 32, QX, XV>;   // g512
+        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, S>;     // g64
+        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, S>;     // g128
+        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, S>;    // g256
+        default: return gemv_dot_kernel<R, KD, 32, QX, XV, S>;   // g512
     }
 }
 
-template <int R, bool QX, int XV>
+template <int R, int S, bool QX, int XV>
 DotFn dot_for_kd(int kd, int lg) {
     switch (kd) {
-        case 3: return dot_for_lg<R, 3, QX, XV>(lg);
-        case 4: return dot_for_lg<R, 4, QX, XV>(lg);
-        case 5: return dot_for_lg<R, 5, QX, XV>(lg);
-        case 8: return dot_for_lg<R, 8, QX, XV>(lg);
-        default: return dot_for_lg<R, 10, QX, XV>(lg);
+        case 3: return dot_for_lg<R, S, 3, QX, XV>(lg);
+        case 4: return dot_for_lg<R, S, 4, QX, XV>(lg);
+        default: return dot_for_lg<R, S, 5, QX, XV>(lg);
     }
 }
 
 // XV: activation chunks per thread, 1 or 3 for int8 codes (K <= 4096 / 12288),
 // 2 or 5 for fp16 input (K <= 4096 / 10240); larger K use a tail loop.
-template <int R>
+template <int R, int S>
 DotFn dot_for(bool qx, int K, int kd, int lg) {
-    if (qx) return K <= 4096 ? dot_for_kd<R, true, 2>(kd, lg) : dot_for_kd<R, true, 5>(kd, lg);
-    return K <= 4096 ? dot_for_kd<R, false, 1>(kd, lg) : dot_for_kd<R, false, 3>(kd, lg);
+    if (qx)
+        return K <= 4096 ? dot_for_kd<R, S, true, 2>(kd, lg) : dot_for_kd<R, S, true, 5>(kd, lg);
+    return K <= 4096 ? dot_for_kd<R, S, false, 1>(kd, lg) : dot_for_kd<R, S, false, 3>(kd, lg);
 }
 
 template <bool D>
@@ -483,15 +542,19 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
         if (lgroups > 64 / R) return GemvPlan{};
         const int PB = (64 / R) * 16;
         const int passes = (K + PB - 1) / PB;
-        // ring depth: every pass of a row in flight when it fits (items flow
-        // on into the next row either way)
+        // split long rows over wave pairs when there are too few row streams
+        // to give every SIMD four or more (the down projection)
+        p.split = (M / R < 4096 && passes >= 8) ? 2 : 1;
+        const int ph = (passes + p.split - 1) / p.split;
         // ring depth: all passes of a row when they are few, else 5 (deeper
         // rings cost more occupancy than they gain, measured on MI355X)
-        p.kd = passes <= 3 ? 3 : passes <= 4 ? 4 : 5;
-        p.grid = ceil_div(M, kDotWaves * R);    // row blocks; capped at launch
+        p.kd = ph <= 3 ? 3 : ph <= 4 ? 4 : 5;
+        p.grid = ceil_div(M, kDotWaves / p.split * R);   // row blocks
         p.block = kDotWaves * 64;
         const int Kp = (K + 15) & ~15;
         p.lds = (size_t)Kp + (size_t)(2 * G) * sizeof(float);
+        if (p.split == 2)   // all terms of a row block, double-buffered, 16-byte aligned
+            p.lds += 16 + (size_t)2 * (kDotWaves / 2) * R * ((G + 3) & ~3) * sizeof(float);
         if (g < 16) return GemvPlan{};
         if (p.lds > 64 * 1024) return GemvPlan{};
         int lg = 0;
@@ -521,16 +584,6 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
     return GemvPlan{};
 }
 
-int dot_resident_blocks(DotFn fn, size_t lds) {
-    int dev = 0, cus = 256, occ = 1;
-    if (hipGetDevice(&dev) == hipSuccess)
-        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kDotWaves * 64, lds) != hipSuccess ||
-        occ < 1)
-        occ = 1;
-    return cus * occ;
-}
-
 hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
                        const int8_t* x_q, const float* x_scale, const uint16_t* X,
                        const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
@@ -540,7 +593,10 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
     if (p.kind == 1 || p.kind == 2) {
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)
-        DotFn fn = p.kind == 1 ? dot_for<1>(qx, K, p.kd, lgl) : dot_for<2>(qx, K, p.kd, lgl);
+        DotFn fn = p.kind == 1 ? (p.split == 2 ? dot_for<1, 2>(qx, K, p.kd, lgl)
+                                               : dot_for<1, 1>(qx, K, p.kd, lgl))
+                               : (p.split == 2 ? dot_for<2, 2>(qx, K, p.kd, lgl)
+                                               : dot_for<2, 1>(qx, K, p.kd, lgl));
         // one workgroup per row block (the cursor also serves a smaller grid)
         const int grid = p.grid;
         hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,

@@ -236,6 +236,9 @@ def test_config3_prefill_subblock(name, N, g):
 
 @pytest.mark.parametrize("N,M,K,g", [
     (1, 100, 512, 64),      # partial 16-row tile
+    (1, 70, 2560, 256),     # N = 1, rows split over wave pairs, odd pass count
+    (1, 33, 9728, 64),      # N = 1 split, ragged last pass, g64
+    (1, 4100, 1536, 128),   # N = 1, two rows per wave and split
     (16, 48, 64, 64),       # one K step
     (3, 16, 4096, 4096),    # g == K (one group, 1-D scale)
     (2, 40, 128, 0),        # group_size <= 0 -> K
