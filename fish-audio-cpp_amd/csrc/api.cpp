@@ -84,7 +84,7 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
                      int rows, int tok0, int toks, int M, int N, int K, hipStream_t stream) {
     const bool aligned = aligned16(W) && aligned16(xq);
     if (aligned && N <= 16) {
-        fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G);
+        fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G, false);
         if (p.kind != 0) {
             FA_HIP(fa::launch_gemv(p, W, w_scale, xq, xs, nullptr, nullptr, nullptr, Y, dbg, row0,
                                    rows, tok0, toks, M, N, K, g, G, stream));
@@ -182,7 +182,7 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     const int G = (K + g - 1) / g;
     if (N == 1 && aligned16(W)) {
         // decode: the GEMV quantizes the token itself (one launch, no scratch)
-        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G);
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true);
         if (gp.kind == 1 || gp.kind == 2) {
             FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, X, act_scale, smooth_inv, Y,
                                    nullptr, 0, 0, 0, 0, M, N, K, g, G, s));

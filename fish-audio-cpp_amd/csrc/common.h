@@ -88,7 +88,6 @@ struct GemvPlan {
     int kind = 0;    // 1, 2: dot kernel with 1 or 2 rows per wave; 3: MFMA kernel
                      // (dot: grid = row blocks)
     int kd = 0;      // dot: passes in flight per wave
-    int split = 1;   // dot: waves sharing one row (1 or 2)
     int lg = 0;      // dot: log2(group size)
     int passes = 0;  // dot: passes per row
     int spg = 0;     // mfma: 64-byte K steps per group
@@ -96,7 +95,8 @@ struct GemvPlan {
     int grid = 0, block = 0;
     size_t lds = 0;
 };
-GemvPlan plan_gemv(int M, int N, int K, int g, int G);
+// qx: the dot kernel quantizes the fp16 token itself (N == 1 only).
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
 // [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to

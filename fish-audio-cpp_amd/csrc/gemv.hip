@@ -48,7 +48,8 @@ __device__ __forceinline__ v4i ld16(const int8_t* p) { return *reinterpret_cast<
 
 // ------------------------------------------------------------ N == 1 ----
 
-constexpr int kDotWaves = 4;   // waves per workgroup
+constexpr int kDotWaves = 4;     // waves per workgroup, staged int8 codes
+constexpr int kDotWavesQx = 8;   // waves per workgroup, in-kernel quantization
 
 // Sum of an int over aligned blocks of LG lanes (all lanes get the block sum).
 // LG <= 16 stays inside a 16-lane DPP row: quad_perm swaps, then half-row and
@@ -69,6 +70,25 @@ __device__ __forceinline__ int group_sum(int p, int lg_rt) {
     }
 }
 
+// Max of a non-negative float over aligned blocks of 2^lgl lanes (runtime
+// width; all lanes get the block max).  Within 16-lane DPP rows one
+// v_max_f32_dpp per step; wider blocks add xor shuffles across rows.  The
+// max is exact in any order.
+template <int CTL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float block_max(float m, int lgl) {
+    if (lgl >= 1) m = fmaxf(m, dpp_f<0xB1>(m));    // quad_perm [1,0,3,2]
+    if (lgl >= 2) m = fmaxf(m, dpp_f<0x4E>(m));    // quad_perm [2,3,0,1]
+    if (lgl >= 3) m = fmaxf(m, dpp_f<0x141>(m));   // row_half_mirror
+    if (lgl >= 4) m = fmaxf(m, dpp_f<0x140>(m));   // row_mirror
+    if (lgl >= 5) m = fmaxf(m, __shfl_xor(m, 16, 64));
+    if (lgl >= 6) m = fmaxf(m, __shfl_xor(m, 32, 64));
+    return m;
+}
+
 // One wave streams R rows (R = 1, 2 or 4; 64/R lanes per row, 16 bytes per
 // lane per pass).  After 4 v_dot4 per lane, lanes of one K-group (LG = g/16
 // of them) sum their partials with DPP, so every lane of a group holds the
@@ -84,19 +104,14 @@ __device__ __forceinline__ int group_sum(int p, int lg_rt) {
 // the first weight loads are in flight; otherwise it stages the given int8
 // activations and fp32 scales.  Either way x_q [K] and x_scale [G] sit in LDS.
 //
-// Work: row blocks of (kDotWaves / S) * R rows; block b, b + gridDim.x, ...
-// belong to workgroup b.  A uniform cursor (row block, pass) walks the wave's
-// passes in order and the weight ring is KD passes ahead of the consumer.  g is
-// a power of two (lg_g = log2 g) with 16 <= g <= 16 * 64/R.
-//
-// S = 2 splits every row's passes over a pair of waves (more, shorter streams
-// for long rows).  Both waves then leave their terms float(P_g) * ws in LDS
-// (double-buffered by row block); after a barrier at the end of the row block
-// the first wave runs the fp32 chain over all G groups in order, four terms
-// and scales per LDS read.  Both waves run the same number of passes (the
-// second may end with empty ones), so every wave meets the same barriers.
-template <int R, int KD, int LG, bool QX, int XV, int S = 1, int kAb = 0>
-__global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
+// Work: row blocks of NWV * R rows (NWV waves per workgroup); block b,
+// b + gridDim.x, ... belong to workgroup b.  A uniform cursor (row block,
+// pass) walks the wave's passes in order and the weight ring is KD passes
+// ahead of the consumer.  g is a power of two (lg_g = log2 g) with
+// 16 <= g <= 16 * 64/R.  With QX every workgroup quantizes the whole token,
+// so QX launches use 8-wave workgroups (half as many copies of that work).
+template <int R, int KD, int LG, bool QX, int XV, int NWV = kDotWaves, int kAb = 0>
+__global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
     const uint16_t* __restrict__ X, const uint16_t* __restrict__ act_scale,
@@ -106,26 +121,15 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     constexpr int RL = 64 / R;            // lanes per row
     constexpr int PB = RL * 16;           // bytes of a row per pass
     constexpr int GPP = RL / LG;          // groups per row per pass
-    constexpr int NT = kDotWaves * 64;
-    constexpr int RS = kDotWaves / S;     // row slots per block
+    constexpr int NT = NWV * 64;
     static_assert(LG >= 1 && LG <= RL, "group must fit a row's lanes");
-    static_assert(S == 1 || S == 2, "split");
     extern __shared__ __align__(16) float lds[];
     const int Kp = (K + 15) & ~15;
     int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                  // [Kp]
-    float* xs_s = lds + Kp / 4;                                      // [G]
-    int* gmax = reinterpret_cast<int*>(xs_s + G);                    // [G] (QX)
+    float* xs_s = lds + Kp / 4;                                      // [G], padded to 4
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int half = S == 2 ? (wave & 1) : 0;
-    const int wslot = S == 2 ? (wave >> 1) : wave;
-    const int PH = S == 2 ? (passes + 1) >> 1 : passes;              // passes per wave and row
-    const int pbase = half * PH;
-    // S == 2: terms of every group in LDS, [2][RS * R][TG], chained at row end
-    constexpr bool DEF = S == 2;
-    const int TG = (G + 3) & ~3;                                      // term slots per row
-    float* terms = lds + ((Kp / 4 + 2 * G + 3) & ~3);                // 16-byte aligned
 
     const int rsub = lane / RL;
     const int li = lane % RL;
@@ -158,13 +162,13 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     v4i a[KD];
     uint16_t sc[KD];
     const v4i zero = {0, 0, 0, 0};
-    auto row_of_blk = [&](int blk) { return (blk * RS + wslot) * R + rsub; };
+    auto row_of_blk = [&](int blk) { return (blk * NWV + wave) * R + rsub; };
     auto load = [&](int slot) {
         const bool live = l_blk < nblocks;
         const int row = row_of_blk(live ? l_blk : blockIdx.x);
         const int rowc = row < M ? row : M - 1;
         const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
-        const int k = (pbase + l_pass) * PB + lane_k;
+        const int k = l_pass * PB + lane_k;
         const bool ok = live && k < K;
         const int kk = ok ? k : 0;
         // no select on the loaded value (that would wait for the load here):
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
         else
             sc[slot] = (uint16_t)kk;
         a[slot] = wa;
-        if (++l_pass == PH) {
+        if (++l_pass == passes) {
             l_pass = 0;
             l_blk += gridDim.x;
         }
@@ -196,78 +200,65 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
             *reinterpret_cast<v4i*>(xq_s + k) = ld16(x_q + k);
         for (int i = tid + NT; i < G; i += NT) xs_s[i] = x_scale[i];
     } else {
-        // per-group |v| maxima (exact in any order), scales, then int8 codes
-        for (int i = tid; i < G; i += NT) gmax[i] = 0;
-        __syncthreads();
-        auto vals = [&](int k, const v4i& raw, float (&v)[8]) {
+        // Chunk c holds x[8c, 8c + 8); chunk c of thread tid is tid + i * NT,
+        // so a K-group (g / 8 chunks) lies in g / 8 consecutive lanes of one
+        // wave.  Its |v| maximum (exact in any order) comes from xor
+        // shuffles, then scale and int8 codes are formed in registers: no
+        // atomics and a single barrier before the codes are read.
+        const int glanes = 1 << (lg_g - 3);
+        auto chunk = [&](int c, const v4i& raw) {
+            const int k = c * 8;
+            const bool ok = k < K;
             const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+            float v[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 v[e] = h2f(h[e]);
-                if (smooth_inv) v[e] *= h2f(smooth_inv[k + e]);
+                if (smooth_inv) v[e] *= h2f(smooth_inv[ok ? k + e : e]);
             }
-        };
-        auto amax_chunk = [&](int k, const v4i& raw) {
-            float v[8];
-            vals(k, raw, v);
-            float m = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-            atomicMax(&gmax[k >> lg_g], __float_as_int(m));   // |v| >= 0: int order == float order
-        };
-        auto quant_chunk = [&](int k, const v4i& raw) {
-            float v[8];
-            vals(k, raw, v);
-            const float inv = 1.0f / xs_s[k >> lg_g];
-            int q[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
-            uint2 u;
-            u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                  ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
-            u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
-                  ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
-            *reinterpret_cast<uint2*>(xq_s + k) = u;
-        };
-        if (!act_scale) {
-#pragma unroll
-            for (int c = 0; c < XV; ++c) {
-                const int k = (tid + c * NT) * 8;
-                if (k < K) amax_chunk(k, xr[c]);
-            }
-            for (int k = (tid + XV * NT) * 8; k < K; k += NT * 8)
-                amax_chunk(k, *reinterpret_cast<const v4i*>(X + k));
-            __syncthreads();
-        }
-        for (int i = tid; i < G; i += NT) {
-            float s;
+            const int gi = ok ? k >> lg_g : G - 1;
+            float sc_;
             if (act_scale) {
-                s = h2f(act_scale[i]);
-                s = s < 1e-8f ? 1e-8f : s;
+                sc_ = h2f(act_scale[gi]);
+                sc_ = sc_ < 1e-8f ? 1e-8f : sc_;
             } else {
-                s = act_scale_from_amax(__int_as_float(gmax[i]));
-            }
-            xs_s[i] = s;
-        }
-        __syncthreads();
+                float m = 0.0f;
 #pragma unroll
-        for (int c = 0; c < XV; ++c) {
-            const int k = (tid + c * NT) * 8;
-            if (k < K) quant_chunk(k, xr[c]);
+                for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+                if (!ok) m = 0.0f;
+                m = block_max(m, lg_g - 3);
+                sc_ = act_scale_from_amax(m);
+            }
+            if (ok) {
+                const float inv = 1.0f / sc_;
+                int q[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
+                uint2 u;
+                u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                      ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+                u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
+                      ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
+                *reinterpret_cast<uint2*>(xq_s + k) = u;
+                if ((c & (glanes - 1)) == 0) xs_s[gi] = sc_;
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < XV; ++i) chunk(tid + i * NT, xr[i]);
+        for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
+            const int c = c0 + tid;
+            chunk(c, *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8)));
         }
-        for (int k = (tid + XV * NT) * 8; k < K; k += NT * 8)
-            quant_chunk(k, *reinterpret_cast<const v4i*>(X + k));
     }
     if constexpr ((kAb & 1) == 0) __syncthreads();
 
     // ---- consume
     int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
-    int tbuf = 0;                           // terms buffer of the current row block
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     auto consume = [&](int slot) {
-        const int kbase = (pbase + c_pass) * PB;       // row offset of this pass (uniform)
+        const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
         const int k = kbase + lane_k;
         v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
         if (k >= K) b = zero;
@@ -284,9 +275,6 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
         }
         if constexpr ((kAb & 4) != 0) {
             acc[0] += term;
-        } else if constexpr (DEF) {
-            if ((li & (LG - 1)) == 0 && k < K)
-                terms[(tbuf * RS * R + wslot * R + rsub) * TG + (k >> lg_g)] = term;
         } else {
             // group order within the pass: slot j of every row; the pass's
             // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
@@ -316,32 +304,12 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
                 }
             }
         }
-        if (++c_pass == PH) {
+        if (++c_pass == passes) {
             const int row = row_of_blk(c_blk);
-            if constexpr (DEF) {
-                if constexpr (S == 2) __syncthreads();
-                if (half == 0) {
-                    // every group in order, four terms and scales per LDS read
-                    const float* t = terms + (size_t)(tbuf * RS * R + wslot * R) * TG;
-                    for (int g4 = 0; g4 < G; g4 += 4) {
-                        const float4 xv = *reinterpret_cast<const float4*>(xs_s + g4);
-                        const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const float4 tv = *reinterpret_cast<const float4*>(t + r * TG + g4);
-                            const float te[4] = {tv.x, tv.y, tv.z, tv.w};
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (g4 + e < G) acc[r] = __builtin_fmaf(te[e], xe[e], acc[r]);
-                        }
-                    }
-                }
-                if constexpr (S == 2) tbuf ^= 1;
-            }
             // lane r*RL (li == 0) of row slot r stores that row
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (rsub == r && li == 0 && half == 0 && row < M) Y[row] = f2h(acc[r]);
+                if (rsub == r && li == 0 && row < M) Y[row] = f2h(acc[r]);
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = 0.0f;
             c_pass = 0;
@@ -351,7 +319,7 @@ __global__ __launch_bounds__(kDotWaves * 64) void gemv_dot_kernel(
     // Rounds that refill the ring, then a last round that only drains it (so
     // every load is unconditional and the wait counts stay exact).
     const int my_blocks = (nblocks - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-    const int items = my_blocks * PH;
+    const int items = my_blocks * passes;
     int base = 0;
     for (; base + KD < items; base += KD) {
 #pragma unroll
@@ -467,32 +435,35 @@ using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const floa
                        const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,
                        int, int, int, int, int, int);
 
-template <int R, int S, int KD, bool QX, int XV>
+template <int R, int KD, bool QX, int XV, int NWV>
 DotFn dot_for_lg(int lg) {
     switch (lg) {
-        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, S>;     // g64
-        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, S>;     // g128
-        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, S>;    // g256
-        default: return gemv_dot_kernel<R, KD, 32, QX, XV, S>;   // g512
+        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, NWV>;     // g64
+        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, NWV>;     // g128
+        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, NWV>;    // g256
+        default: return gemv_dot_kernel<R, KD, 32, QX, XV, NWV>;   // g512
     }
 }
 
-template <int R, int S, bool QX, int XV>
+template <int R, bool QX, int XV, int NWV>
 DotFn dot_for_kd(int kd, int lg) {
     switch (kd) {
-        case 3: return dot_for_lg<R, S, 3, QX, XV>(lg);
-        case 4: return dot_for_lg<R, S, 4, QX, XV>(lg);
-        default: return dot_for_lg<R, S, 5, QX, XV>(lg);
+        case 3: return dot_for_lg<R, 3, QX, XV, NWV>(lg);
+        case 4: return dot_for_lg<R, 4, QX, XV, NWV>(lg);
+        default: return dot_for_lg<R, 5, QX, XV, NWV>(lg);
     }
 }
 
-// XV: activation chunks per thread, 1 or 3 for int8 codes (K <= 4096 / 12288),
-// 2 or 5 for fp16 input (K <= 4096 / 10240); larger K use a tail loop.
-template <int R, int S>
+// Staged int8 codes: 4 waves, XV = 1 or 3 16-byte chunks per thread
+// (K <= 4096 / 12288).  In-kernel quantization: 8 waves, XV = 1 or 3 chunks of
+// 8 fp16 values per thread (K <= 4096 / 12288).  Larger K use a tail loop.
+template <int R>
 DotFn dot_for(bool qx, int K, int kd, int lg) {
     if (qx)
-        return K <= 4096 ? dot_for_kd<R, S, true, 2>(kd, lg) : dot_for_kd<R, S, true, 5>(kd, lg);
-    return K <= 4096 ? dot_for_kd<R, S, false, 1>(kd, lg) : dot_for_kd<R, S, false, 3>(kd, lg);
+        return K <= 4096 ? dot_for_kd<R, true, 1, kDotWavesQx>(kd, lg)
+                         : dot_for_kd<R, true, 3, kDotWavesQx>(kd, lg);
+    return K <= 4096 ? dot_for_kd<R, false, 1, kDotWaves>(kd, lg)
+                     : dot_for_kd<R, false, 3, kDotWaves>(kd, lg);
 }
 
 template <bool D>
@@ -533,7 +504,7 @@ int round_maxg(int m) {
 
 }  // namespace
 
-GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx) {
     GemvPlan p{};
     if (N == 1 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 16 == 0 && K <= 32768) {
         const int lgroups = g / 16;
@@ -542,19 +513,14 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G) {
         if (lgroups > 64 / R) return GemvPlan{};
         const int PB = (64 / R) * 16;
         const int passes = (K + PB - 1) / PB;
-        // split long rows over wave pairs when there are too few row streams
-        // to give every SIMD four or more (the down projection)
-        p.split = (M / R < 4096 && passes >= 8) ? 2 : 1;
-        const int ph = (passes + p.split - 1) / p.split;
         // ring depth: all passes of a row when they are few, else 5 (deeper
         // rings cost more occupancy than they gain, measured on MI355X)
-        p.kd = ph <= 3 ? 3 : ph <= 4 ? 4 : 5;
-        p.grid = ceil_div(M, kDotWaves / p.split * R);   // row blocks
-        p.block = kDotWaves * 64;
+        p.kd = passes <= 3 ? 3 : passes <= 4 ? 4 : 5;
+        const int nwv = qx ? kDotWavesQx : kDotWaves;
+        p.grid = ceil_div(M, nwv * R);   // row blocks
+        p.block = nwv * 64;
         const int Kp = (K + 15) & ~15;
-        p.lds = (size_t)Kp + (size_t)(2 * G) * sizeof(float);
-        if (p.split == 2)   // all terms of a row block, double-buffered, 16-byte aligned
-            p.lds += 16 + (size_t)2 * (kDotWaves / 2) * R * ((G + 3) & ~3) * sizeof(float);
+        p.lds = (size_t)Kp + (size_t)((G + 3) & ~3) * sizeof(float);   // xs padded for float4 reads
         if (g < 16) return GemvPlan{};
         if (p.lds > 64 * 1024) return GemvPlan{};
         int lg = 0;
@@ -593,10 +559,8 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
     if (p.kind == 1 || p.kind == 2) {
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)
-        DotFn fn = p.kind == 1 ? (p.split == 2 ? dot_for<1, 2>(qx, K, p.kd, lgl)
-                                               : dot_for<1, 1>(qx, K, p.kd, lgl))
-                               : (p.split == 2 ? dot_for<2, 2>(qx, K, p.kd, lgl)
-                                               : dot_for<2, 1>(qx, K, p.kd, lgl));
+        if (qx != (p.block == kDotWavesQx * 64)) return hipErrorInvalidValue;   // planned for the other input
+        DotFn fn = p.kind == 1 ? dot_for<1>(qx, K, p.kd, lgl) : dot_for<2>(qx, K, p.kd, lgl);
         // one workgroup per row block (the cursor also serves a smaller grid)
         const int grid = p.grid;
         hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,
