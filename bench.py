@@ -36,19 +36,6 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def event_time_ms(fn, reps, torch):
-    """Average duration of fn() measured with events on the current stream."""
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    times = []
-    for _ in range(reps):
-        s.record()
-        fn()
-        e.record()
-        e.synchronize()
-        times.append(s.elapsed_time(e))
-    return times
-
-
 def cpu_baseline(stack, torch, budget_s):
     """configs[1] on the host: the C oracle (scalar C restatement of the
     reference's W8A8 math, OpenMP over output rows) for one layer's four
@@ -93,6 +80,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate_up GEMV event timing (for rocprofv3 runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the configs[3] M=2048 g256 prefill GEMMs (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -105,6 +94,9 @@ def main():
     from fish_amd.synth import LAYER_SHAPES
 
     torch.cuda.init()
+    if args.prefill_only:
+        print(json.dumps(prefill_tops(torch, ops, [(256, 2048)])), flush=True)
+        return
     log("building 36-layer g256 weight set ...")
     st = DecodeStack(n_layers=args.layers, g=256, tokens=1, seed=0)
     torch.cuda.synchronize()
@@ -257,28 +249,39 @@ def run_secondary(torch, ops, st, args):
     torch.cuda.empty_cache()
 
     # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
+    out.update(prefill_tops(torch, ops, [(256, 512), (256, 2048), (64, 2048)]))
+    return out
+
+
+def prefill_tops(torch, ops, cases):
+    """int8 TOPS of w8a8_gemm_quantized (scale-table launch + GEMM)
+    on the four layer shapes, for each (group size, tokens) case; random
+    weights and activations (the MFMA clock depends on the data)."""
+    from fish_amd.synth import LAYER_SHAPES
+    out = {}
     gen = torch.Generator(device="cuda")
     gen.manual_seed(3)
-    for g in (256, 64):
-        for M in ((512, 2048) if g == 256 else (2048,)):
-            tot_ops, tot_ms = 0.0, 0.0
-            for name, (K, N) in LAYER_SHAPES.items():
-                w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
-                W, S = ops.quantize_weights_groupwise(w, g)
-                del w
-                x = torch.randn((M, K), generator=gen, device="cuda").half()
-                xq, xs = ops.quantize_activations(x, g)
-                y = torch.empty((M, N), device="cuda", dtype=torch.float16)
-                f = lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=y)
-                f()
-                ms = statistics.median(event_time_ms(f, 5, torch))
-                o = 2.0 * M * N * K
-                tot_ops += o
-                tot_ms += ms
-                out["cfg3_gemm_m%d_g%d_%s_TOPS" % (M, g, name)] = round(o / (ms * 1e-3) / 1e12, 1)
-            tops = tot_ops / (tot_ms * 1e-3) / 1e12
-            out["cfg3_gemm_m%d_g%d_layer_TOPS" % (M, g)] = round(tops, 1)
-            out["cfg3_gemm_m%d_g%d_frac_int8_peak" % (M, g)] = round(tops / INT8_PEAK_TOPS, 4)
+    for g, M in cases:
+        tot_ops, tot_ms = 0.0, 0.0
+        for name, (K, N) in LAYER_SHAPES.items():
+            w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+            W, S = ops.quantize_weights_groupwise(w, g)
+            del w
+            x = torch.randn((M, K), generator=gen, device="cuda").half()
+            xq, xs = ops.quantize_activations(x, g)
+            y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+            f = lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=y)
+            # both launches of the call (scale tables + GEMM), 8 calls per
+            # graph, so host launch overhead stays out of the GPU time
+            ms = graph_us_per_call(torch, [f] * 8, reps=5) * 1e-3
+            o = 2.0 * M * N * K
+            tot_ops += o
+            tot_ms += ms
+            out["cfg3_gemm_m%d_g%d_%s_TOPS" % (M, g, name)] = round(o / (ms * 1e-3) / 1e12, 1)
+            out["cfg3_gemm_m%d_g%d_%s_us" % (M, g, name)] = round(ms * 1e3, 2)
+        tops = tot_ops / (tot_ms * 1e-3) / 1e12
+        out["cfg3_gemm_m%d_g%d_layer_TOPS" % (M, g)] = round(tops, 1)
+        out["cfg3_gemm_m%d_g%d_frac_int8_peak" % (M, g)] = round(tops / INT8_PEAK_TOPS, 4)
     return out
 
 

@@ -21,8 +21,6 @@
 //   the group's scales ride along with its first stage into LDS.
 #include "common.h"
 
-#include <algorithm>
-
 namespace fa {
 namespace {
 
@@ -210,24 +208,27 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(
 // Group-major scale tables for the pipelined kernel: wsT [G][M] (weight
 // scales widened to fp32, exact) and xsT [G][N].  With them the 128 scales of
 // one tile and group are one contiguous 512-byte run instead of 128 strided
-// words.
+// words.  Block b transposes `tr` consecutive rows (weight rows, then tokens)
+// through LDS: the rows' G scales are one contiguous run in the source, and
+// each group's `tr` outputs are contiguous in the table.
 __global__ __launch_bounds__(256) void scale_tables_kernel(const uint16_t* __restrict__ w_scale,
                                                            const float* __restrict__ x_scale,
                                                            float* __restrict__ wsT,
                                                            float* __restrict__ xsT, int M, int N,
-                                                           int G) {
-    const size_t nw = (size_t)G * M;
-    const size_t total = nw + (size_t)G * N;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * 256) {
-        if (i < nw) {
-            const size_t gi = i / M, r = i % M;
-            wsT[i] = h2f(w_scale[G == 1 ? r : r * G + gi]);
-        } else {
-            const size_t j = i - nw;
-            const size_t gi = j / N, t = j % N;
-            xsT[j] = x_scale[t * G + gi];
-        }
+                                                           int G, int tr, int wblocks) {
+    extern __shared__ float tile[];   // [tr][G]
+    const bool isw = (int)blockIdx.x < wblocks;
+    const int rows = isw ? M : N;
+    const int r0 = (isw ? blockIdx.x : blockIdx.x - wblocks) * tr;
+    const int nr = min(tr, rows - r0);
+    const int n = nr * G;
+    for (int i = threadIdx.x; i < n; i += 256)
+        tile[i] = isw ? h2f(w_scale[(size_t)r0 * G + i]) : x_scale[(size_t)r0 * G + i];
+    __syncthreads();
+    float* dst = isw ? wsT : xsT;
+    for (int i = threadIdx.x; i < tr * G; i += 256) {
+        const int gi = i / tr, r = i % tr;
+        if (r < nr) dst[(size_t)gi * rows + r0 + r] = tile[r * G + gi];
     }
 }
 
@@ -590,7 +591,8 @@ bool gemm_pipe_ok(int M, int N, int K, int g) {
     (void)M;
     (void)N;
     // g a power of two >= 64, K a whole number of 128-byte stages (>= 4)
-    return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 256 && g <= K;
+    // (and at most 8192 groups, so one row's scales fit the transpose tile)
+    return g >= 64 && (g & (g - 1)) == 0 && K % 128 == 0 && K >= 256 && g <= K && K / g <= 8192;
 }
 
 size_t gemm_pipe_tables_bytes(int M, int N, int G) {
@@ -606,10 +608,13 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
     while ((64 << lg_spg) < g) ++lg_spg;
     float* const wsT = tables;
     float* const xsT = tables + (size_t)G * M;
-    const size_t total = (size_t)G * ((size_t)M + (size_t)N);
-    const unsigned pblocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(scale_tables_kernel, dim3(pblocks), dim3(256), 0, stream, w_scale, x_scale,
-                       wsT, xsT, M, N, G);
+    // rows per transpose block: up to 64, with the block's scales <= 32 KB of LDS
+    int tr = 64;
+    while (tr > 1 && (size_t)tr * G * sizeof(float) > 32768) tr >>= 1;
+    const int wblocks = ceil_div(M, tr);
+    hipLaunchKernelGGL(scale_tables_kernel, dim3((unsigned)(wblocks + ceil_div(N, tr))), dim3(256),
+                       (size_t)tr * G * sizeof(float), stream, w_scale, x_scale, wsT, xsT, M, N, G,
+                       tr, wblocks);
     // 128 x BN tiles, 128-byte K stages, 2-deep ring, two workgroups per CU.
     // BN = 64 when 128-token tiles would number fewer than the 256 CUs.
     const int tm = ceil_div(M, 128);
