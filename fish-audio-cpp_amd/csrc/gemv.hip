@@ -337,7 +337,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
 
 constexpr int kTile = 16;
 
-template <int SPG, int MAXG, bool kDbg>
+template <int SPG, int MAXG, bool kDbg, int kAb = 0>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
@@ -360,26 +360,45 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int lr = lane & 15;            // A: weight row in tile; B: token
     const int kq = (lane >> 4) * 16;
     const int row_ld = min(row0 + lr, M - 1);
-    const bool tok_ok = lr < N;
     const size_t kbase = (size_t)gb * SPG * 64 + kq;
     const int8_t* wp = W + (size_t)row_ld * K + kbase;
-    const int8_t* xp = x_q + (size_t)(tok_ok ? lr : 0) * K + kbase;
+    // token lanes past N read token N-1: their MFMA columns are never stored
+    const int8_t* xp = x_q + (size_t)min(lr, N - 1) * K + kbase;
 
     v4i a[KD], b[KD];
     const v4i zero = {0, 0, 0, 0};
+    // unconditional loads, no select on the loaded data: a select would make
+    // the compiler wait for each load right where it is issued
     auto load = [&](int slot, int step) {
         const size_t off = (size_t)(step < nsteps ? step : 0) * 64;
         a[slot] = ld16(wp + off);
-        b[slot] = tok_ok ? ld16(xp + off) : zero;
+        if constexpr ((kAb & 1) == 0) b[slot] = ld16(xp + off);
+        else b[slot] = a[slot];
     };
+    // Scales of the tile's 16 rows and of the tokens, all groups: at most 5
+    // per thread (the plan keeps G <= 20 * NW).  Their loads go out before
+    // the weight ring's, so the wait before the LDS stores covers only them.
+    // Token rows past N repeat token N-1 (their outputs are never stored).
+    constexpr int kSt = 5;
+    uint16_t wsr[kSt];
+    float xsr[kSt];
 #pragma unroll
-    for (int s = 0; s < KD; ++s) load(s, s);
-
-    for (int i = threadIdx.x; i < kTile * G; i += blockDim.x) {
+    for (int q = 0; q < kSt; ++q) {
+        const int i = min((int)threadIdx.x + q * (int)blockDim.x, kTile * G - 1);
         const int r = i / G, gi = i - r * G;
         const int row = min(row0 + r, M - 1);
-        ws_s[i] = h2f(G == 1 ? w_scale[row] : w_scale[(size_t)row * G + gi]);
-        xs_s[i] = r < N ? x_scale[(size_t)r * G + gi] : 0.0f;
+        wsr[q] = w_scale[G == 1 ? (size_t)row : (size_t)row * G + gi];
+        xsr[q] = x_scale[(size_t)min(r, N - 1) * G + gi];
+    }
+#pragma unroll
+    for (int s = 0; s < KD; ++s) load(s, s);
+#pragma unroll
+    for (int q = 0; q < kSt; ++q) {
+        const int i = threadIdx.x + q * blockDim.x;
+        if ((kAb & 4) == 0 && i < kTile * G) {
+            ws_s[i] = h2f(wsr[q]);
+            xs_s[i] = xsr[q];
+        }
     }
     __syncthreads();
 
@@ -409,16 +428,33 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
         }
     }
 
+    // this lane's token scales for the wave's groups, read before the chain
+    // (the chain's LDS writes would otherwise keep these reads inside it)
+    float xsv[MAXG];
+#pragma unroll
+    for (int j = 0; j < MAXG; ++j) xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
+
     // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
     // the previous wave's sums over its own groups.
-    for (int w = 0; w < NW; ++w) {
+    if constexpr ((kAb & 2) != 0) {   // timing probe: unordered, no barriers
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < MAXG; ++j)
+                if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
+            if (wave == 0) chain[lr * kTile + orow + r] = acc;
+        }
+        __syncthreads();
+    }
+    for (int w = 0; w < ((kAb & 2) ? 0 : NW); ++w) {
         if (wave == w) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float acc = w == 0 ? 0.0f : chain[lr * kTile + orow + r];
 #pragma unroll
                 for (int j = 0; j < MAXG; ++j)
-                    if (j < ng) acc = __builtin_fmaf(terms[j][r], xs_s[lr * G + gb + j], acc);
+                    if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
                 chain[lr * kTile + orow + r] = acc;
             }
         }
