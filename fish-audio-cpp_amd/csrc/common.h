@@ -91,7 +91,8 @@ struct GemvPlan {
     int lg = 0;      // dot: log2(group size)
     int passes = 0;  // dot: passes per row
     int spg = 0;     // mfma: 64-byte K steps per group
-    int maxg = 0;    // mfma: groups per wave (register-resident terms)
+    int maxg = 0;    // mfma: groups per wave
+    bool lc = false; // mfma: all terms in LDS, one chain lane per output
     int grid = 0, block = 0;
     size_t lds = 0;
 };

@@ -337,7 +337,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
 
 constexpr int kTile = 16;
 
-template <int SPG, int MAXG, bool kDbg, int kAb = 0>
+template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
@@ -347,7 +347,10 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     extern __shared__ float lds[];
     float* ws_s = lds;                   // [16 rows][G]
     float* xs_s = lds + kTile * G;       // [16 tokens][G]
-    float* chain = lds + 2 * kTile * G;  // [16 tokens][16 rows]
+    float* chain = lds + 2 * kTile * G;  // [16 tokens][16 rows] (!LC)
+    // LC: every term float(P_g) * ws in LDS, [G][ns tokens][16 rows]
+    const int ns = N <= 8 ? 8 : 16;
+    float* tl = lds + 2 * kTile * G;
 
     const int NW = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6;
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     __syncthreads();
 
     const int orow = 4 * (lane >> 4);    // this lane's 4 output rows: orow .. orow+3
-    float terms[MAXG][4];
+    float terms[LC ? 1 : MAXG][4];
 #pragma unroll
     for (int j = 0; j < MAXG; ++j) {
         v4i P = zero;
@@ -415,8 +418,16 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
             load(slot, step + KD);
         }
         const int gi = gb + (j < ng ? j : 0);
+        if constexpr (LC) {
+            if (j < ng && lr < ns) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) terms[j][r] = (float)P[r] * ws_s[(orow + r) * G + gi];
+                for (int r = 0; r < 4; ++r)
+                    tl[(gi * ns + lr) * kTile + orow + r] = (float)P[r] * ws_s[(orow + r) * G + gi];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) terms[j][r] = (float)P[r] * ws_s[(orow + r) * G + gi];
+        }
         if constexpr (kDbg) {
             if (j < ng && lr < N) {
 #pragma unroll
@@ -428,41 +439,42 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
         }
     }
 
-    // this lane's token scales for the wave's groups, read before the chain
-    // (the chain's LDS writes would otherwise keep these reads inside it)
-    float xsv[MAXG];
-#pragma unroll
-    for (int j = 0; j < MAXG; ++j) xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
-
-    // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
-    // the previous wave's sums over its own groups.
-    if constexpr ((kAb & 2) != 0) {   // timing probe: unordered, no barriers
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
+    if constexpr (LC) {
+        // one lane per output runs the whole chain in group order
+        __syncthreads();
+        for (int t = threadIdx.x; t < kTile * N; t += blockDim.x) {
+            const int r = t & (kTile - 1), tok = t >> 4;
             float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < MAXG; ++j)
-                if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
-            if (wave == 0) chain[lr * kTile + orow + r] = acc;
+            for (int gi = 0; gi < G; ++gi)
+                acc = __builtin_fmaf(tl[(gi * ns + tok) * kTile + r], xs_s[tok * G + gi], acc);
+            if (row0 + r < M) Y[(size_t)tok * M + row0 + r] = f2h(acc);
         }
-        __syncthreads();
-    }
-    for (int w = 0; w < ((kAb & 2) ? 0 : NW); ++w) {
-        if (wave == w) {
+    } else {
+        // this lane's token scales for the wave's groups, read before the chain
+        // (the chain's LDS writes would otherwise keep these reads inside it)
+        float xsv[MAXG];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float acc = w == 0 ? 0.0f : chain[lr * kTile + orow + r];
+        for (int j = 0; j < MAXG; ++j) xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
+
+        // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
+        // the previous wave's sums over its own groups.
+        for (int w = 0; w < NW; ++w) {
+            if (wave == w) {
 #pragma unroll
-                for (int j = 0; j < MAXG; ++j)
-                    if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
-                chain[lr * kTile + orow + r] = acc;
+                for (int r = 0; r < 4; ++r) {
+                    float acc = w == 0 ? 0.0f : chain[lr * kTile + orow + r];
+#pragma unroll
+                    for (int j = 0; j < MAXG; ++j)
+                        if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
+                    chain[lr * kTile + orow + r] = acc;
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
-    }
-    for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
-        const int t = i / kTile, r = i - t * kTile;
-        if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
+        for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
+            const int t = i / kTile, r = i - t * kTile;
+            if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
+        }
     }
 }
 
@@ -506,29 +518,34 @@ template <bool D>
 using MfmaFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*, uint16_t*,
                         DbgWindow, int, int, int, int);
 
-template <int SPG, bool D>
+template <int SPG, bool LC, bool D>
 MfmaFn<D> mfma_for_maxg(int maxg) {
     switch (maxg) {
-        case 1: return gemv_mfma_kernel<SPG, 1, D>;
-        case 2: return gemv_mfma_kernel<SPG, 2, D>;
-        case 3: return gemv_mfma_kernel<SPG, 3, D>;
-        case 4: return gemv_mfma_kernel<SPG, 4, D>;
-        case 6: return gemv_mfma_kernel<SPG, 6, D>;
-        case 8: return gemv_mfma_kernel<SPG, 8, D>;
-        case 12: return gemv_mfma_kernel<SPG, 12, D>;
-        case 16: return gemv_mfma_kernel<SPG, 16, D>;
-        default: return gemv_mfma_kernel<SPG, 20, D>;
+        case 1: return gemv_mfma_kernel<SPG, 1, LC, D>;
+        case 2: return gemv_mfma_kernel<SPG, 2, LC, D>;
+        case 3: return gemv_mfma_kernel<SPG, 3, LC, D>;
+        case 4: return gemv_mfma_kernel<SPG, 4, LC, D>;
+        case 6: return gemv_mfma_kernel<SPG, 6, LC, D>;
+        case 8: return gemv_mfma_kernel<SPG, 8, LC, D>;
+        case 12: return gemv_mfma_kernel<SPG, 12, LC, D>;
+        case 16: return gemv_mfma_kernel<SPG, 16, LC, D>;
+        default: return gemv_mfma_kernel<SPG, 20, LC, D>;
+    }
+}
+
+template <bool LC, bool D>
+MfmaFn<D> mfma_for_spg(int spg, int maxg) {
+    switch (spg) {
+        case 1: return mfma_for_maxg<1, LC, D>(maxg);
+        case 2: return mfma_for_maxg<2, LC, D>(maxg);
+        case 4: return mfma_for_maxg<4, LC, D>(maxg);
+        default: return mfma_for_maxg<8, LC, D>(maxg);
     }
 }
 
 template <bool D>
-MfmaFn<D> mfma_for(int spg, int maxg) {
-    switch (spg) {
-        case 1: return mfma_for_maxg<1, D>(maxg);
-        case 2: return mfma_for_maxg<2, D>(maxg);
-        case 4: return mfma_for_maxg<4, D>(maxg);
-        default: return mfma_for_maxg<8, D>(maxg);
-    }
+MfmaFn<D> mfma_for(bool lc, int spg, int maxg) {
+    return lc ? mfma_for_spg<true, D>(spg, maxg) : mfma_for_spg<false, D>(spg, maxg);
 }
 
 int round_maxg(int m) {
@@ -567,9 +584,11 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx) {
     }
     if (N >= 1 && N <= 16 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 64 == 0) {
         const int tiles = ceil_div(M, kTile);
-        // waves per 16-row tile: enough for ~2048 waves in flight, at most 8,
-        // each holding at most 20 groups' terms in registers
-        int nw = ceil_div(2048, tiles);
+        // Waves per 16-row tile (measured on MI355X): with many tiles two
+        // waves split the groups; with few tiles (o and down projections) up
+        // to eight, and the terms go through LDS to one chain lane per output.
+        // A wave holds at most 20 groups.
+        int nw = tiles >= 384 ? 2 : (G >= 64 ? 8 : 2);
         if (nw < ceil_div(G, 20)) nw = ceil_div(G, 20);
         if (nw > G) nw = G;
         if (nw > 8) nw = 8;
@@ -579,7 +598,10 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx) {
         p.maxg = round_maxg(ceil_div(G, nw));
         p.grid = tiles;
         p.block = nw * 64;
-        p.lds = (size_t)(2 * kTile * G + kTile * kTile) * sizeof(float);
+        const int ns = N <= 8 ? 8 : 16;
+        const size_t lds_lc = (size_t)(2 * kTile * G + G * ns * kTile) * sizeof(float);
+        p.lc = tiles < 384 && lds_lc <= 64 * 1024;
+        p.lds = p.lc ? lds_lc : (size_t)(2 * kTile * G + kTile * kTile) * sizeof(float);
         if (p.lds > 64 * 1024) return GemvPlan{};
         return p;
     }
@@ -605,10 +627,10 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
         if (X) return hipErrorInvalidValue;
         const bool d = dbg_partials != nullptr;
         if (d)
-            hipLaunchKernelGGL(mfma_for<true>(p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
+            hipLaunchKernelGGL(mfma_for<true>(p.lc, p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
                                stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
         else
-            hipLaunchKernelGGL(mfma_for<false>(p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
+            hipLaunchKernelGGL(mfma_for<false>(p.lc, p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
                                stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
     } else {
         return hipErrorInvalidValue;
