@@ -232,7 +232,8 @@ int fa_rms_norm(const uint16_t* x, const uint16_t* weight, uint16_t* out, int n_
     if (n_tokens == 0) return FA_OK;
     if (!x || !weight || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
     if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
-    FA_HIP(fa::launch_rms_norm_quant(x, weight, eps, nullptr, nullptr, dim, 1, nullptr, nullptr,
+    FA_HIP(fa::launch_rms_norm_quant(const_cast<uint16_t*>(x), nullptr, weight, eps, nullptr,
+                                     nullptr, dim, 1, nullptr, nullptr,
                                      out, n_tokens, dim, (hipStream_t)stream));
     return FA_OK;
 }
@@ -251,8 +252,28 @@ int fa_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
     if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
     const int g = eff_group(dim, group_size);
     const int G = (dim + g - 1) / g;
-    FA_HIP(fa::launch_rms_norm_quant(x, weight, eps, smooth_inv, act_scale, g, G, X_q, X_scale, out,
+    FA_HIP(fa::launch_rms_norm_quant(const_cast<uint16_t*>(x), nullptr, weight, eps, smooth_inv,
+                                     act_scale, g, G, X_q, X_scale, out,
                                      n_tokens, dim, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_residual_rms_norm_quant(uint16_t* h, const uint16_t* resid, const uint16_t* weight,
+                               float eps, const uint16_t* smooth_inv, const uint16_t* act_scale,
+                               int group_size, int8_t* X_q, float* X_scale, uint16_t* out,
+                               int n_tokens, int dim, void* stream) {
+    const char* fn = "fa_residual_rms_norm_quant";
+    g_err.clear();
+    if (n_tokens < 0 || dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad n_tokens=%d dim=%d", fn, n_tokens, dim);
+    if (n_tokens == 0) return FA_OK;
+    if (!h || !resid || !weight || !X_q || !X_scale)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
+    const int g = eff_group(dim, group_size);
+    const int G = (dim + g - 1) / g;
+    FA_HIP(fa::launch_rms_norm_quant(h, resid, weight, eps, smooth_inv, act_scale, g, G, X_q,
+                                     X_scale, out, n_tokens, dim, (hipStream_t)stream));
     return FA_OK;
 }
 

@@ -337,13 +337,15 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
 
 constexpr int kTile = 16;
 
-template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0>
+template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0, int kKD = 12>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G) {
     constexpr int NSTEP = SPG * MAXG;
-    constexpr int KD = NSTEP < 8 ? NSTEP : 8;
+    // ring depth: kKD steps, 8 when 16+ groups' terms are held in registers
+    constexpr int KDM = (!LC && MAXG >= 16) ? 8 : kKD;
+    constexpr int KD = NSTEP < KDM ? NSTEP : KDM;
     extern __shared__ float lds[];
     float* ws_s = lds;                   // [16 rows][G]
     float* xs_s = lds + kTile * G;       // [16 tokens][G]

@@ -119,6 +119,42 @@ __global__ __launch_bounds__(kThreads) void quantize_act_kernel(
     const int k1 = active ? min(k0 + g, K) : k0;
     const size_t row = (size_t)n * K;
 
+    if (g <= lanes * VEC) {
+        // one VEC chunk per lane covers the group: the prologue values are
+        // formed once and kept in registers for the max and the codes
+        const int k = k0 + sub * VEC;
+        const bool ok = k < k1;
+        float v[VEC];
+        uint16_t h[VEC];
+        if (ok) {
+            prologue_values<VEC, P>(X, up, smooth_inv, row + k, k, v, h);
+        } else {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) v[i] = 0.0f;
+        }
+        float s;
+        if (act_scale) {
+            s = h2f(act_scale[gi]);
+            s = s < 1e-8f ? 1e-8f : s;
+        } else {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            amax = subgroup_max_rt(amax, lg);
+            s = act_scale_from_amax(amax);
+        }
+        if (active && sub == 0) x_scale[(size_t)n * G + gi] = s;
+        if (ok) {
+            const float inv = 1.0f / s;
+            int q[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) q[i] = quant_rn(v[i], inv);
+            store_q<VEC>(x_q + row + k, q);
+            if (P == Prologue::kSiluMul && out_f16) store_h<VEC>(out_f16 + row + k, h);
+        }
+        return;
+    }
+
     float s;
     if (act_scale) {
         s = h2f(act_scale[gi]);
@@ -165,7 +201,8 @@ int lanes_log2_for(int g, int vec) {
 // sums are reduced by the same tree.  rsqrtf is replaced by a double 1/sqrt.
 // The normalised fp16 row is then quantized per K-group straight from LDS.
 __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ weight, float eps,
+    uint16_t* __restrict__ x, const uint16_t* __restrict__ resid,
+    const uint16_t* __restrict__ weight, float eps,
     const uint16_t* __restrict__ smooth_inv, const uint16_t* __restrict__ act_scale,
     int8_t* __restrict__ x_q, float* __restrict__ x_scale, uint16_t* __restrict__ out_f16,
     int dim, int T, int g, int G, int lg, int vec8) {
@@ -175,12 +212,52 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
     const int tid = threadIdx.x;
     const size_t base = (size_t)blockIdx.x * dim;
 
-    float local = 0.0f;
-    if (tid < T)
-        for (int i = tid; i < dim; i += T) {
-            float v = h2f(x[base + i]);
-            local = __builtin_fmaf(v, v, local);
+    // Thread t holds x[t], x[t + T], ... (at most kNV of them when
+    // dim <= kNV * T, else the loop re-reads x); all its loads, gamma's
+    // included, go out before the first use, so the row costs one memory
+    // latency.  With `resid`, x is first replaced by fp16(x + resid) in
+    // place (residual_add, ffn_activations.cu:41-45).
+    constexpr int kNV = 8;
+    const bool regs = dim <= kNV * T;
+    float xv[kNV], gv[kNV];
+    if (regs) {
+        uint16_t xr[kNV], rr[kNV], gr[kNV];
+#pragma unroll
+        for (int j = 0; j < kNV; ++j) {
+            const int i = min(tid + j * T, dim - 1);
+            xr[j] = x[base + i];
+            gr[j] = weight[i];
+            if (resid) rr[j] = resid[base + i];
         }
+#pragma unroll
+        for (int j = 0; j < kNV; ++j) {
+            xv[j] = h2f(xr[j]);
+            if (resid) {
+                const uint16_t hs = f2h(xv[j] + h2f(rr[j]));
+                xv[j] = h2f(hs);
+                if (tid < T && tid + j * T < dim) x[base + tid + j * T] = hs;
+            }
+            gv[j] = h2f(gr[j]);
+        }
+    } else if (resid) {
+        for (int i = tid; i < dim; i += blockDim.x)
+            x[base + i] = f2h(h2f(x[base + i]) + h2f(resid[base + i]));
+        __syncthreads();
+    }
+
+    float local = 0.0f;
+    if (tid < T) {
+        if (regs) {
+#pragma unroll
+            for (int j = 0; j < kNV; ++j)
+                if (tid + j * T < dim) local = __builtin_fmaf(xv[j], xv[j], local);
+        } else {
+            for (int i = tid; i < dim; i += T) {
+                float v = h2f(x[base + i]);
+                local = __builtin_fmaf(v, v, local);
+            }
+        }
+    }
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) local += __shfl_down(local, off, 32);
     if ((tid & 31) == 0) s_warp[tid >> 5] = local;
@@ -197,10 +274,22 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
     }
     __syncthreads();
     const float r = s_rms;
-    for (int i = tid; i < dim; i += blockDim.x) {
-        uint16_t h = f2h((h2f(x[base + i]) * r) * h2f(weight[i]));
-        s_row[i] = h;
-        if (out_f16) out_f16[base + i] = h;
+    if (regs && blockDim.x == T) {
+#pragma unroll
+        for (int j = 0; j < kNV; ++j) {
+            const int i = tid + j * T;
+            if (i < dim) {
+                const uint16_t h = f2h((xv[j] * r) * gv[j]);
+                s_row[i] = h;
+                if (out_f16) out_f16[base + i] = h;
+            }
+        }
+    } else {
+        for (int i = tid; i < dim; i += blockDim.x) {
+            uint16_t h = f2h((h2f(x[base + i]) * r) * h2f(weight[i]));
+            s_row[i] = h;
+            if (out_f16) out_f16[base + i] = h;
+        }
     }
     if (!x_q) return;
     __syncthreads();
@@ -356,7 +445,8 @@ hipError_t launch_quantize_activations(const uint16_t* X, const uint16_t* up, Pr
     return hipGetLastError();
 }
 
-hipError_t launch_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
+hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint16_t* weight,
+                                 float eps,
                                  const uint16_t* smooth_inv, const uint16_t* act_scale,
                                  int g, int G, int8_t* x_q, float* x_scale, uint16_t* out_f16,
                                  int n_tokens, int dim, hipStream_t stream) {
@@ -368,8 +458,8 @@ hipError_t launch_rms_norm_quant(const uint16_t* x, const uint16_t* weight, floa
                       ((uintptr_t)x_q & 7) == 0;
     const int lg = x_q ? lanes_log2_for(g, vec8 ? 8 : 1) : 0;
     const size_t lds = ((size_t)dim * 2 + 15) & ~(size_t)15;
-    hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(n_tokens), dim3(block), lds, stream, x, weight,
-                       eps, smooth_inv, act_scale, x_q, x_scale, out_f16, dim, T, g, G, lg,
+    hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(n_tokens), dim3(block), lds, stream, x, resid,
+                       weight, eps, smooth_inv, act_scale, x_q, x_scale, out_f16, dim, T, g, G, lg,
                        vec8 ? 1 : 0);
     return hipGetLastError();
 }

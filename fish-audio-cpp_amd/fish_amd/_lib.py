@@ -55,6 +55,7 @@ SIGNATURES = {
     "fa_quantize_activations": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_rms_norm": (_i, [_p, _p, _p, _i, _i, _f, _p]),
     "fa_rms_norm_quant": (_i, [_p, _p, _f, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
+    "fa_residual_rms_norm_quant": (_i, [_p, _p, _p, _f, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
     "fa_silu": (_i, [_p, _i64, _p]),
     "fa_mul": (_i, [_p, _p, _i64, _p]),
     "fa_residual_add": (_i, [_p, _p, _i64, _p]),

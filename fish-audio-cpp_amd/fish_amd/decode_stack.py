@@ -4,8 +4,13 @@ Mirrors the per-layer call order of DualAREngine::decode_step
 (src/engine/dual_ar_engine.cc:576-648) with attention omitted (the o_proj
 input is the q slice of the qkv output):
 
-    rms_norm+quant -> qkv -> quant -> o -> residual
-    -> rms_norm+quant -> gate_up -> silu*mul+quant -> down -> residual
+    rms_norm+quant -> qkv -> quant -> o -> residual+rms_norm+quant
+    -> gate_up -> silu*mul+quant -> down -> (residual+rms_norm+quant of the
+    next layer; a plain residual after the last)
+
+Each residual add is fused into the RMSNorm + quant launch that follows it
+(fa_residual_rms_norm_quant), so a layer takes nine launches, two of which
+(the o-input copy and its quantizer) stand in for attention.
 
 gate_up is w1 and w3 stacked into one [2 * 9728, 2560] weight (exact when the
 two share their input quantization, i.e. no per-weight smooth_inv).
@@ -90,11 +95,17 @@ class DecodeStack:
         l_ = ops.lib()
         s = ops._stream()
         G2560 = (HIDDEN + g - 1) // g
-        for lay in self.layers:
-            # attention_norm + quant -> wqkv
-            ops.check(l_.fa_rms_norm_quant(self.h.data_ptr(), lay["attn_norm"].data_ptr(), 1e-6,
-                                           None, None, g, self.xq.data_ptr(), self.xs.data_ptr(),
-                                           None, T, HIDDEN, s))
+        for li, lay in enumerate(self.layers):
+            # (previous layer's down residual +) attention_norm + quant -> wqkv
+            if li == 0:
+                ops.check(l_.fa_rms_norm_quant(self.h.data_ptr(), lay["attn_norm"].data_ptr(),
+                                               1e-6, None, None, g, self.xq.data_ptr(),
+                                               self.xs.data_ptr(), None, T, HIDDEN, s))
+            else:
+                ops.check(l_.fa_residual_rms_norm_quant(
+                    self.h.data_ptr(), self.y["down"].data_ptr(), lay["attn_norm"].data_ptr(),
+                    1e-6, None, None, g, self.xq.data_ptr(), self.xs.data_ptr(), None, T, HIDDEN,
+                    s))
             L = lay["qkv"]
             ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
                                                 self.xq.data_ptr(), self.xs.data_ptr(),
@@ -108,11 +119,10 @@ class DecodeStack:
             ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
                                                 self.xq.data_ptr(), self.xs.data_ptr(),
                                                 self.y["o"].data_ptr(), L.N, T, L.K, s))
-            ops.check(l_.fa_residual_add(self.h.data_ptr(), self.y["o"].data_ptr(), T * HIDDEN, s))
-            # ffn_norm + quant -> w1|w3
-            ops.check(l_.fa_rms_norm_quant(self.h.data_ptr(), lay["ffn_norm"].data_ptr(), 1e-6,
-                                           None, None, g, self.xq.data_ptr(), self.xs.data_ptr(),
-                                           None, T, HIDDEN, s))
+            # o residual + ffn_norm + quant -> w1|w3
+            ops.check(l_.fa_residual_rms_norm_quant(
+                self.h.data_ptr(), self.y["o"].data_ptr(), lay["ffn_norm"].data_ptr(), 1e-6, None,
+                None, g, self.xq.data_ptr(), self.xs.data_ptr(), None, T, HIDDEN, s))
             L = lay["gate_up"]
             ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
                                                 self.xq.data_ptr(), self.xs.data_ptr(),
@@ -130,8 +140,8 @@ class DecodeStack:
             ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
                                                 self.xq.data_ptr(), self.xs.data_ptr(),
                                                 self.y["down"].data_ptr(), L.N, T, L.K, s))
-            ops.check(l_.fa_residual_add(self.h.data_ptr(), self.y["down"].data_ptr(),
-                                         T * HIDDEN, s))
+        # the last layer's down residual
+        ops.check(l_.fa_residual_add(self.h.data_ptr(), self.y["down"].data_ptr(), T * HIDDEN, s))
         del G2560
 
     def stack_bytes(self):

@@ -102,6 +102,22 @@ def rms_norm_quant(x, weight, eps, group_size, smooth_inv=None, act_scale=None, 
     return (X_q, X_s, out) if want_out else (X_q, X_s)
 
 
+def residual_rms_norm_quant_(h, resid, weight, eps, group_size, smooth_inv=None, act_scale=None,
+                             want_out=False):
+    """h <- fp16(h + resid) in place, then rms_norm_quant of the new h."""
+    _need(h, torch.float16, "h"); _need(resid, torch.float16, "resid")
+    _need(weight, torch.float16, "weight")
+    n, d = h.shape
+    G = num_groups(d, group_size)
+    X_q = torch.empty((n, d), dtype=torch.int8, device=h.device)
+    X_s = torch.empty((n, G), dtype=torch.float32, device=h.device)
+    out = torch.empty_like(h) if want_out else None
+    check(lib().fa_residual_rms_norm_quant(_ptr(h), _ptr(resid), _ptr(weight), eps,
+                                           _ptr(smooth_inv), _ptr(act_scale), group_size,
+                                           _ptr(X_q), _ptr(X_s), _ptr(out), n, d, _stream()))
+    return (X_q, X_s, out) if want_out else (X_q, X_s)
+
+
 def silu_(x):
     _need(x, torch.float16, "x")
     check(lib().fa_silu(_ptr(x), x.numel(), _stream()))

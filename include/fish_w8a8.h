@@ -94,6 +94,16 @@ int fa_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
                       int8_t* X_q, float* X_scale, uint16_t* out,
                       int n_tokens, int dim, void* stream);
 
+/* residual_add fused in front of fa_rms_norm_quant: h <- fp16(h + resid) in
+ * place (residual_add, ffn_activations.cu:41-45), then the normalised, group-
+ * quantized rows of the new h.  Replaces the residual_add, rms_norm and
+ * quantizer launches the reference makes between sublayers
+ * (dual_ar_engine.cc:632-636, and :647 then :580 of the next layer) with one. */
+int fa_residual_rms_norm_quant(uint16_t* h, const uint16_t* resid, const uint16_t* weight,
+                               float eps, const uint16_t* smooth_inv, const uint16_t* act_scale,
+                               int group_size, int8_t* X_q, float* X_scale, uint16_t* out,
+                               int n_tokens, int dim, void* stream);
+
 /* fish::kernels::silu_forward / mul_forward / residual_add
  * (src/kernels/kernels.h:111-140, ffn_activations.cu:139-161), in place on x/a. */
 int fa_silu(uint16_t* x, int64_t n, void* stream);

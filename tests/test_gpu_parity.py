@@ -102,7 +102,8 @@ def test_rms_norm_reference_closed_forms():
     assert np.all(np.abs(out - 2 * x / np.sqrt(5 + 1e-6)) <= 1e-2)
 
 
-@pytest.mark.parametrize("n,dim,g", [(8, 2560, 64), (1, 2560, 256), (3, 100, 48), (2, 4096, 0)])
+@pytest.mark.parametrize("n,dim,g", [(8, 2560, 64), (1, 2560, 256), (3, 100, 48), (2, 4096, 0),
+                                     (2, 9000, 128)])
 @pytest.mark.parametrize("variant", ["dynamic", "static", "smooth"])
 def test_rms_norm_quant_bitexact(n, dim, g, variant):
     x = synth.activations_f16(n, dim, seed=n)
@@ -113,6 +114,24 @@ def test_rms_norm_quant_bitexact(n, dim, g, variant):
     xq, xs, out = ops.rms_norm_quant(dev(x), dev(w), 1e-6, g, smooth_inv=None if sm is None else dev(sm),
                                      act_scale=None if act is None else dev(act), want_out=True)
     rq, rs, rout = ref.rms_norm_quant(x, w, 1e-6, g, smooth_inv=sm, act_scale=act)
+    assert same(host(out), rout)
+    assert same(host(xq), rq)
+    assert same(host(xs), rs)
+
+
+@pytest.mark.parametrize("n,dim,g", [(1, 2560, 256), (8, 2560, 64), (3, 100, 48), (2, 9000, 128)])
+def test_residual_rms_norm_quant_bitexact(n, dim, g):
+    """h <- fp16(h + r) in place, then RMSNorm + group quant of the new h; the
+    fused kernel equals residual_add followed by rms_norm_quant.  dim = 9000
+    exceeds the register path (8 values per thread) and takes the loop."""
+    h = synth.activations_f16(n, dim, seed=n + 7)
+    r = (synth.activations_f16(n, dim, seed=n + 8) * np.float16(0.5)).astype(np.float16)
+    w = synth.gamma_f16(dim)
+    hd = dev(h)
+    xq, xs, out = ops.residual_rms_norm_quant_(hd, dev(r), dev(w), 1e-6, g, want_out=True)
+    rh = ref.residual_add(h, r)
+    rq, rs, rout = ref.rms_norm_quant(rh, w, 1e-6, g)
+    assert same(host(hd), rh)
     assert same(host(out), rout)
     assert same(host(xq), rq)
     assert same(host(xs), rs)
@@ -303,3 +322,31 @@ def test_bin_file_end_to_end():
     x = synth.activations_f16(1, K, seed=32)
     Y = ops.w8a8_gemm(Wd, Sd, dev(x), meta.group_size)
     assert same(host(Y), ref.w8a8_gemm(q, s, g, x)), "bin"
+
+
+# ------------------------------------------------------- decode stack ----
+
+@pytest.mark.parametrize("g,T", [(256, 1), (64, 2)])
+def test_decode_stack_bitexact(g, T):
+    """configs[4] pipeline (fish_amd.decode_stack.run_stack, fused residual +
+    RMSNorm + quant included) over two layers, against the same sequence of
+    oracle functions: the final residual stream is bit-identical."""
+    from fish_amd.decode_stack import DecodeStack, FFN, Q_DIM
+    st = DecodeStack(n_layers=2, g=g, tokens=T, seed=5)
+    st.h.copy_(st.h0)
+    st.run_stack()
+    torch.cuda.synchronize()
+    h = host(st.h0)
+    for lay in st.layers:
+        def lin(name, xq, xs):
+            return ref.gemm_quantized(host(lay[name].W), host(lay[name].scale), g, xq, xs)
+        xq, xs, _ = ref.rms_norm_quant(h, host(lay["attn_norm"]), 1e-6, g)
+        y = lin("qkv", xq, xs)
+        xq, xs = ref.quantize_activations(np.ascontiguousarray(y[:, :Q_DIM]), g)
+        h = ref.residual_add(h, lin("o", xq, xs))
+        xq, xs, _ = ref.rms_norm_quant(h, host(lay["ffn_norm"]), 1e-6, g)
+        y = lin("gate_up", xq, xs)
+        xq, xs, _ = ref.silu_mul_quant(np.ascontiguousarray(y[:, :FFN]),
+                                       np.ascontiguousarray(y[:, FFN:]), g)
+        h = ref.residual_add(h, lin("down", xq, xs))
+    assert same(host(st.h), h)
