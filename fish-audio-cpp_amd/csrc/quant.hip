@@ -63,10 +63,36 @@ __device__ __forceinline__ void store_h(uint16_t* p, const uint16_t (&h)[VEC]) {
     }
 }
 
-// Runtime-width subgroup max (width = 1 << lg, lg <= 6); every lane of the
-// wave must call it.
+template <int CTL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
+}
+
+// Runtime-width subgroup max (width = 1 << lg, lg <= 6; all lanes get it);
+// every lane of the wave must call it.  Within 16-lane rows one DPP op per
+// step, across rows xor shuffles.  The max is exact in any order.
 __device__ __forceinline__ float subgroup_max_rt(float v, int lg) {
-    for (int off = (1 << lg) >> 1; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if (lg >= 1) v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+    if (lg >= 2) v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+    if (lg >= 3) v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+    if (lg >= 4) v = fmaxf(v, dpp_f<0x140>(v));   // row_mirror
+    if (lg >= 5) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if (lg >= 6) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+// The shuffle-down sum tree of a 32-lane CUDA warp (offsets 16, 8, 4, 2, 1,
+// `v += __shfl_down(v, off)`), on each 32-lane half of the wave.  Lane 0 of
+// each half gets exactly the reference's pairing: the cross-row step is a
+// shuffle, the in-row steps are DPP row_shl (lane i reads lane i + off;
+// lanes past the row end read 0, and their sums are never used).
+__device__ __forceinline__ float warp32_sum_down(float v) {
+    v += __shfl_down(v, 16, 32);
+    v += dpp_f<0x108>(v);   // row_shl:8
+    v += dpp_f<0x104>(v);   // row_shl:4
+    v += dpp_f<0x102>(v);   // row_shl:2
+    v += dpp_f<0x101>(v);   // row_shl:1
     return v;
 }
 
@@ -258,15 +284,13 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
             }
         }
     }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) local += __shfl_down(local, off, 32);
+    local = warp32_sum_down(local);
     if ((tid & 31) == 0) s_warp[tid >> 5] = local;
     __syncthreads();
     if (tid < 32) {
         const int nw = (T + 31) >> 5;
         float v = tid < nw ? s_warp[tid] : 0.0f;
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
+        v = warp32_sum_down(v);
         if (tid == 0) {
             float t = v / (float)dim + eps;
             s_rms = (float)(1.0 / sqrt((double)t));
