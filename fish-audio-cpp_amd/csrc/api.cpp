@@ -91,7 +91,8 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
             return FA_OK;
         }
     }
-    if (aligned && fa::gemm_pipe_ok(M, N, K, g)) {
+    const bool tile = aligned && fa::gemm_tile_ok(M, N, K, g);
+    if (tile || (aligned && fa::gemm_pipe_ok(M, N, K, g))) {
         Workspace* ws = nullptr;
         int rc = current_ws(&ws);
         if (rc) return rc;
@@ -99,8 +100,12 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
         rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(M, N, G), stream);
         ws->st = (float*)p;
         if (rc) return rc;
-        FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks, M,
-                                    N, K, g, G, stream));
+        if (tile)
+            FA_HIP(fa::launch_gemm_tile(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks,
+                                        M, N, K, g, G, stream));
+        else
+            FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks,
+                                        M, N, K, g, G, stream));
         return FA_OK;
     }
     if (aligned && K % 64 == 0 && g % 64 == 0) {

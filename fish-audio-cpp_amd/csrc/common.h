@@ -130,6 +130,16 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
                             int K, int g, int G, hipStream_t stream);
 
+// Prefill tile kernel: g in {64, 128, 256}, K % 256 == 0; same scale tables
+// (gemm_pipe_tables_bytes) and the same two launches as launch_gemm_pipe.
+bool gemm_tile_ok(int M, int N, int K, int g);
+// variant: 0 = by shape (gemm_tile_choice), 1 = 256 x 128 tiles, 2 = 128 x 128.
+int gemm_tile_choice(int M, int N, int K, int g);
+hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                            const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
+                            int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
+                            int K, int g, int G, hipStream_t stream, int variant = 0);
+
 // Any-shape fallback (any K, any group size, unaligned pointers).
 hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                                const float* x_scale, uint16_t* Y, int32_t* dbg_partials,

@@ -21,6 +21,8 @@
 //   the group's scales ride along with its first stage into LDS.
 #include "common.h"
 
+#include <type_traits>
+
 namespace fa {
 namespace {
 
@@ -414,6 +416,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 #pragma unroll
         for (int u = 0; u < kNst; ++u) {
             const int s = s0 + u;
+            if (s >= nstages) break;   // nstages need not be a multiple of kNst
             if constexpr ((kAb & 8) == 0) wait_vm<kYounger>();
             __syncthreads();
             // groups starting in stage s + 1: their scales came with stage s
@@ -535,6 +538,350 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
         }
 }
 
+// ---------------------------------------------------------------------------
+// Tile kernel (g = 64, 128 or 256; K % 128 == 0): the prefill workhorse.
+//
+// Workgroup tile BM weight rows x BN tokens, NW = BM * BN / 4096 waves, each
+// wave 64 rows x 64 tokens = 2 x 2 blocks of v_mfma_i32_32x32x32_i8 with the
+// TOKENS in the A operand and the WEIGHT ROWS in the B operand: lane l of a
+// block then holds weight row (l & 31) for 16 tokens, so the row's weight
+// scale is one register per block.  K advances through an NST-deep ring of
+// 128-byte stages filled by direct global->LDS loads, as in gemm_pipe_kernel.
+//
+// Exact two-operation epilogue.  A group's first MFMA starts from the int32
+// constant 0x4B400000 (the bit pattern of 1.5 * 2^23) instead of zero.  For
+// |P| < 2^22 -- always true at g <= 256, where |P| <= 256 * 127^2 -- the
+// finished accumulator, read as an fp32, is exactly 12582912 + P, so
+//     fl(float(P) * ws) = fma(asfloat(acc), ws, -(12582912 * ws))
+// (the fma forms (12582912 + P) * ws - 12582912 * ws = P * ws exactly and
+// rounds once; 12582912 * ws = 3 * 2^22 * ws is exact in fp32 for an fp16
+// ws).  The reference's accumulate step acc = fma(float(P) * ws, xs, acc)
+// (int8_gemm.cu:231) then follows unchanged, group by group in order, so the
+// fp16 output is bit-identical to the oracle's with two VALU operations per
+// output and group instead of three.
+//
+// A group's epilogue runs at the first K step of the next group, each block's
+// scaling next to that block's first MFMA of the new group, so the VALU work
+// of one block overlaps the matrix work of the others.
+// kAb (measurement builds only; 0 in the library): 1 drops the MFMAs, 2 the
+// fragment reads, 4 the epilogue, 8 the global->LDS loads.
+template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, int kAb = 0, bool kSched = true>
+__global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ wsT,
+    const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
+    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G, int tiles_m,
+    int tiles_n) {
+    constexpr int NW = BM * BN / 4096;
+    constexpr int WMN = BM / 64;             // waves along the weight rows
+    constexpr int AJ = BN * 8 / 64 / NW;     // token-tile loads per wave and stage
+    constexpr int BJ = BM * 8 / 64 / NW;     // weight-tile loads per wave and stage
+    static_assert(AJ * NW * 64 == BN * 8 && BJ * NW * 64 == BM * 8, "load split");
+    static_assert((BM + BN) % 64 == 0 && (BM + BN) / 64 <= NW, "scale loads");
+    constexpr int kPerStage = AJ + BJ + 2;
+    constexpr int kYounger = (NST - 2) * kPerStage;
+    constexpr int NSS = 8;                   // scale ring: group gi in slot gi & 7
+    constexpr float kMagicF = 12582912.0f;   // 1.5 * 2^23
+    constexpr int kMagicI = 0x4B400000;
+
+    __shared__ __align__(16) int8_t At[NST][BN * 128];   // tokens, 128 B per row and stage
+    __shared__ __align__(16) int8_t Bt[NST][BM * 128];   // weight rows
+    __shared__ __align__(16) float sc[NSS][BM + BN];     // [0, BM) weight scales, then tokens
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WMN;
+    const int wn = wave / WMN;
+
+    const int ntiles = tiles_m * tiles_n;
+    const int b = blockIdx.x;
+    int t = b;
+    if (ntiles % 8 == 0) t = (b % 8) * (ntiles / 8) + b / 8;
+    const int tm = t / tiles_n;
+    const int tn = t % tiles_n;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    uint32_t aoff[AJ], boff[BJ];
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+        const int q = (j * NW + wave) * 64 + lane;
+        const int row = q >> 3;
+        const int c = (q & 7) ^ swz<2>(row);
+        aoff[j] = (uint32_t)(min(n0 + row, N - 1) - n0) * (uint32_t)K + c * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+        const int q = (j * NW + wave) * 64 + lane;
+        const int row = q >> 3;
+        const int c = (q & 7) ^ swz<2>(row);
+        boff[j] = (uint32_t)(min(m0 + row, M - 1) - m0) * (uint32_t)K + c * 16;
+    }
+    const int8_t* const abase = x_q + (size_t)n0 * K;
+    const int8_t* const bbase = W + (size_t)m0 * K;
+    // scale fetch of thread tid: weight row m0 + tid for tid < BM, else token
+    // n0 + (tid - BM) % BN; waves past (BM + BN) / 64 repeat a token wave's
+    // fetch (same words to the same LDS slots), so every wave issues the same
+    // number of loads.
+    const int stk = (tid - BM) % BN;
+    const int sslot = wave < (BM + BN) / 64 ? wave : BM / 64 + (wave - BM / 64) % (BN / 64);
+    const float* const ssrc = tid < BM ? wsT + min(m0 + tid, M - 1)
+                                       : xsT + min(n0 + (stk < 0 ? stk + BN : stk), N - 1);
+    const size_t sstride = tid < BM ? (size_t)M : (size_t)N;
+
+    const int nsub = K >> 6;                 // 64-byte substeps
+    const int nst = nsub >> 1;               // 128-byte stages
+
+    // Stage st's tiles into ring slot u, plus the scales of the groups that
+    // start in stage st (two fetches; a stage with fewer starting groups
+    // re-fetches one of its groups into the same slot).  Stages past the end
+    // re-fetch the last stage so every wave's load count stays uniform.
+    auto issue = [&](int st, int u) {
+        if constexpr ((kAb & 8) != 0) return;
+        const int sc_st = min(max(st, 0), nst - 1);
+        const size_t koff = (size_t)sc_st * 128;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j)
+            dma16_so(abase + koff, aoff[j], lds_addr(&At[u][(j * NW + wave) * 1024]));
+#pragma unroll
+        for (int j = 0; j < BJ; ++j)
+            dma16_so(bbase + koff, boff[j], lds_addr(&Bt[u][(j * NW + wave) * 1024]));
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int gn = (2 * sc_st + q) >> LGS;
+            dma4(ssrc + (size_t)gn * sstride, lds_addr(&sc[gn & (NSS - 1)][sslot * 64]));
+        }
+    };
+
+
+    v16i P[2][2];
+    float acc[2][2][16];
+    v16i magic;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) magic[e] = kMagicI;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                P[i][j][e] = kMagicI;
+                acc[i][j][e] = 0.0f;
+            }
+    // held in registers once: otherwise the compiler re-creates the constant
+    // in each block's accumulator registers (16 moves per block and group)
+    asm volatile("" : "+v"(magic));
+
+    const int fr = lane & 31;
+    const int fh = lane >> 5;
+    const int arow0 = wn * 64 + fr;          // token row of A block 0 in the tile
+    const int brow0 = wm * 64 + fr;          // weight row of B block 0 in the tile
+    // byte offset of this lane's fragment row at K chunk 0 (plus its half-wave
+    // chunk fh), swizzled; chunk q*4 + kk*2 is then a XOR of (q*4 + kk*2) * 16,
+    // because the row base has zeros in bits 4-6 and fh occupies bit 0 of the
+    // chunk index
+    uint32_t alane[2], blane[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ra = arow0 + i * 32, rb = brow0 + i * 32;
+        alane[i] = (uint32_t)(ra * 128 + ((fh ^ swz<2>(ra)) * 16));
+        blane[i] = (uint32_t)(rb * 128 + ((fh ^ swz<2>(rb)) * 16));
+    }
+
+    // Scales of one group in registers: the weight scale of this lane's row in
+    // each B block, its -(12582912 * ws), and the 16 token scales of each A
+    // block.  They are read from LDS one group ahead (right after the previous
+    // epilogue), so the epilogue itself never waits on LDS.
+    struct Scales {
+        float ws[2], nws[2];
+        float4 xs[2][4];
+    };
+    auto load_scales = [&](int gi, Scales& sv) {
+        const float* s = sc[gi & (NSS - 1)];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            sv.ws[j] = s[brow0 + j * 32];
+            sv.nws[j] = -(kMagicF * sv.ws[j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sv.xs[i][r] =
+                    *reinterpret_cast<const float4*>(&s[BM + wn * 64 + i * 32 + 8 * r + 4 * fh]);
+    };
+    // scale group gi's finished accumulators of block (i, j) into acc
+    auto epi = [&](int gi, const Scales& sv, int i, int j) {
+        if constexpr ((kAb & 4) != 0) return;
+        const float ws = sv.ws[j];
+        const float nws = sv.nws[j];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float xs[4] = {sv.xs[i][r].x, sv.xs[i][r].y, sv.xs[i][r].z, sv.xs[i][r].w};
+            float tv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                tv[c] = __builtin_fmaf(__int_as_float(P[i][j][4 * r + c]), ws, nws);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = 4 * r + c;
+                acc[i][j][e] = __builtin_fmaf(tv[c], xs[c], acc[i][j][e]);
+                if constexpr (kDbg) {
+                    const int row = m0 + brow0 + j * 32;
+                    const int tok = n0 + wn * 64 + i * 32 + 8 * r + 4 * fh + c;
+                    if (row < M && tok < N && dbg.in(row, tok))
+                        dbg.at(row, tok, gi, G) = P[i][j][e] - kMagicI;
+                }
+            }
+        }
+    };
+    // Before the first group the accumulators hold the bare constant: with all
+    // scales 0 its "epilogue" adds fma(fma(c, 0, -0), 0, acc) = acc exactly.
+    Scales sv;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sv.ws[j] = sv.nws[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv.xs[i][r] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // One 128-byte stage s held in ring slot U % NST.  U is the stage's index
+    // within an unrolled run that starts at an even stage, so the ring slot and
+    // every group boundary (SPG substeps per group) are compile-time.
+    constexpr int SPG = 1 << LGS;            // 64-byte substeps per group
+    auto stage = [&](auto uc, int s) {
+        constexpr int u = decltype(uc)::value;
+        if (s < 0) return;   // padding stage before the first run: nothing to do
+        const int slot = u % NST;
+        wait_vm<kYounger>();
+        __syncthreads();
+        issue(s + NST - 1, (u + NST - 1) % NST);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int tsub = 2 * s + q;
+            const bool fresh = ((2 * u + q) % SPG) == 0;   // == (tsub % SPG == 0)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                v4i a[2], bb[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    // row * 128 + 16 * ((q * 4 + kk * 2 + fh) ^ swz(row)), formed
+                    // here (the fence keeps the compiler from holding all of
+                    // these per slot in registers across the loop)
+                    uint32_t off = alane[i] ^ (uint32_t)((q * 4 + kk * 2) * 16);
+                    asm volatile("" : "+v"(off));
+                    if constexpr ((kAb & 2) == 0)
+                        a[i] = *reinterpret_cast<const v4i*>(&At[slot][off]);
+                    else
+                        a[i] = v4i{(int)off, q, s, 0x01020304};
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t off = blane[j] ^ (uint32_t)((q * 4 + kk * 2) * 16);
+                    asm volatile("" : "+v"(off));
+                    if constexpr ((kAb & 2) == 0)
+                        bb[j] = *reinterpret_cast<const v4i*>(&Bt[slot][off]);
+                    else
+                        bb[j] = v4i{kk, (int)off, 0x05060708, s};
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (kk == 0 && fresh) {
+                    // New group: its first MFMAs start from the constant
+                    // (issued first, independent of the epilogue), then the
+                    // previous group's epilogue.  At the first step there is
+                    // no previous group: the accumulators still hold the bare
+                    // constant, which scales to exactly 0 with group 0's
+                    // (finite) scales.
+                    const int gcur = tsub >> LGS;
+                    const int gprev = max(gcur - 1, 0);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            // block (i, j): scale the finished group in place,
+                            // then restart its accumulators; the MFMA of one
+                            // block runs under the scaling of the next
+                            epi(gprev, sv, i, j);
+                            if constexpr ((kAb & 1) == 0)
+                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], magic,
+                                                                                0, 0, 0);
+                            else
+                                P[i][j] = magic ^ a[i].x ^ bb[j].y;
+                            if constexpr (!kDbg && kSched) {
+                                __builtin_amdgcn_sched_group_barrier(0x100, 5, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x002, 33, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            }
+                        }
+                    // this group's scales landed with this stage
+                    load_scales(gcur, sv);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            if constexpr ((kAb & 1) == 0)
+                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                                    a[i], bb[j], P[i][j], 0, 0, 0);
+                            else
+                                P[i][j][0] ^= a[i].x ^ bb[j].y;
+                        }
+                }
+            }
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I5 = std::integral_constant<int, 5>;
+    // Runs of UF = lcm(NST, 2) stages.  When UF does not divide the stage
+    // count, numbering starts at -pad (pad even, < UF): stages below 0 are
+    // skipped (no loads beyond the prologue's, no MFMAs), so every run has
+    // the same compile-time slot and group pattern.
+    constexpr int UF = NST % 2 == 0 ? NST : 2 * NST;
+    static_assert(UF == 2 || UF == 4 || UF == 6, "unroll");
+    const int pad = (UF - nst % UF) % UF;
+    // stage s lives in ring slot (s + pad) % NST
+#pragma unroll
+    for (int u = 0; u < NST - 1; ++u) issue(u, (u + pad) % NST);
+    for (int s0 = -pad; s0 < nst; s0 += UF) {
+        stage(I0{}, s0);
+        stage(I1{}, s0 + 1);
+        if constexpr (UF >= 4) {
+            stage(I2{}, s0 + 2);
+            stage(I3{}, s0 + 3);
+        }
+        if constexpr (UF >= 6) {
+            stage(I4{}, s0 + 4);
+            stage(I5{}, s0 + 5);
+        }
+    }
+    wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
+    // the last group's scales were loaded at its first stage
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) epi(G - 1, sv, i, j);
+
+    // fp16 out: lane (row) writes 16 tokens per block; the 32 lanes of a
+    // half-wave cover 64 contiguous bytes of one token's output row
+    const int row_b = m0 + brow0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = row_b + j * 32;
+        if (row >= M) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int tok = n0 + wn * 64 + i * 32 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                if (tok < N) Y[(size_t)tok * M + row] = f2h(acc[i][j][e]);
+            }
+    }
+}
+
 // Any K, any group size, any alignment: one wave per (row, token); lanes
 // stride the group, the int32 partial is reduced exactly across the wave and
 // scaled in the reference order.  Used only for shapes the MFMA kernels do
@@ -637,6 +984,68 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
             hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, 2, 2, false>), grid, dim3(256), 0,
                                stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, lg_spg, G, tm, tn);
     }
+    return hipGetLastError();
+}
+
+bool gemm_tile_ok(int M, int N, int K, int g) {
+    (void)M;
+    (void)N;
+    return (g == 64 || g == 128 || g == 256) && K % 256 == 0 && g <= K;
+}
+
+int gemm_tile_choice(int M, int N, int K, int g) {
+    // Measured on MI355X over the layer shapes at 512 and 2048 tokens:
+    // 128 x 128 tiles (two 4-wave workgroups per CU, whose group epilogues
+    // drift apart) win at g64 and on mid-size grids; 256 x 128 tiles (one
+    // 8-wave workgroup, 25 % less tile traffic per MFMA) win on large grids
+    // and long K.  The 128 x 128 build at g128 does not fit its registers, so
+    // g128 always takes 256 x 128.
+    if (g == 128) return 1;
+    if (g == 64) return 2;
+    const size_t t256 = (size_t)ceil_div(M, 256) * ceil_div(N, 128);
+    return (t256 >= 1024 || (K >= 8192 && t256 >= 128)) ? 1 : 2;
+}
+
+hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
+                            const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
+                            int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
+                            int K, int g, int G, hipStream_t stream, int variant) {
+    DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
+    int lg_spg = 0;
+    while ((64 << lg_spg) < g) ++lg_spg;
+    float* const wsT = tables;
+    float* const xsT = tables + (size_t)G * M;
+    int tr = 64;
+    while (tr > 1 && (size_t)tr * G * sizeof(float) > 32768) tr >>= 1;
+    const int wblocks = ceil_div(M, tr);
+    hipLaunchKernelGGL(scale_tables_kernel, dim3((unsigned)(wblocks + ceil_div(N, tr))), dim3(256),
+                       (size_t)tr * G * sizeof(float), stream, w_scale, x_scale, wsT, xsT, M, N, G,
+                       tr, wblocks);
+    if (variant == 0) variant = gemm_tile_choice(M, N, K, g);
+    const int bm = variant == 1 ? 256 : 128;
+    const int tm = ceil_div(M, bm);
+    const int tn = ceil_div(N, 128);
+    const dim3 grid((unsigned)(tm * tn));
+#define FA_TILE(BMV, NSTV, OCCV, LGS)                                                            \
+    if (dbg_partials)                                                                            \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true>), grid,            \
+                           dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, tm,   \
+                           tn);                                                                  \
+    else                                                                                         \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false>), grid,           \
+                           dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, tm,   \
+                           tn);
+#define FA_TILE_G(BMV, NSTV, OCCV)                                                               \
+    if (lg_spg == 0) { FA_TILE(BMV, NSTV, OCCV, 0) }                                             \
+    else if (lg_spg == 1) { FA_TILE(BMV, NSTV, OCCV, 1) }                                        \
+    else { FA_TILE(BMV, NSTV, OCCV, 2) }
+    if (variant == 1) {
+        FA_TILE_G(256, 3, 1)
+    } else {
+        FA_TILE_G(128, 2, 2)
+    }
+#undef FA_TILE_G
+#undef FA_TILE
     return hipGetLastError();
 }
 

@@ -265,6 +265,10 @@ def test_config3_prefill_subblock(name, N, g):
     (4, 64, 1024, 128),     # g128: two MFMA steps per group
     (17, 130, 256, 128),    # first GEMM size, ragged tiles
     (300, 200, 512, 512),   # GEMM, ragged tokens
+    (300, 260, 512, 256),   # tile kernel, ragged tokens and rows
+    (40, 300, 768, 64),     # tile kernel, g64 (two groups per stage)
+    (129, 520, 1280, 128),  # tile kernel, g128
+    (33, 64, 384, 128),     # K % 256 == 128: pipelined kernel, odd stage count
     (3, 40, 100, 48),       # K, g not multiples of 64: generic kernel
     (20, 33, 96, 32),       # generic kernel, N > 16
 ])
