@@ -52,6 +52,8 @@ struct Workspace {
     size_t xs_bytes = 0;
     float* st = nullptr;        // group-major scale tables of the pipelined GEMM
     size_t st_bytes = 0;
+    uint16_t* yt = nullptr;     // fp16 [N, 2F] of the SwiGLU entry's separate-launch path
+    size_t yt_bytes = 0;
 };
 
 thread_local std::unordered_map<int, Workspace> g_ws;
@@ -185,7 +187,7 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W)) {
+    if (N == 1 && aligned16(W) && aligned16(X)) {
         // decode: the GEMV quantizes the token itself (one launch, no scratch)
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true);
         if (gp.kind == 1 || gp.kind == 2) {
@@ -206,6 +208,159 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     ws->xs = (float*)p;
     if (rc) return rc;
     FA_HIP(fa::launch_quantize_activations(X, nullptr, fa::Prologue::kPlain, act_scale, smooth_inv,
+                                           ws->xq, ws->xs, nullptr, N, K, g, G, s));
+    return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
+                            s);
+}
+
+// [a, a + n) and [b, b + m) overlap (fp16 element counts)
+static bool overlaps(const uint16_t* a, size_t n, const uint16_t* b, size_t m) {
+    return a && b && a < b + m && b < a + n;
+}
+
+int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
+                     const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
+                     const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
+                     uint16_t* Y, int M, int N, int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_rms";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !x || !gamma || !Y)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (resid && !h_out)
+        return fail(FA_ERR_INVALID_ARG, "%s: a residual addend needs h_out", fn);
+    const size_t nk = (size_t)N * (size_t)K;
+    if (h_out && (overlaps(h_out, nk, x, nk) || overlaps(h_out, nk, resid, nk)))
+        return fail(FA_ERR_INVALID_ARG, "%s: h_out overlaps x or resid", fn);
+    if (K > 65536) return fail(FA_ERR_INVALID_ARG, "%s: K=%d exceeds 65536", fn, K);
+    hipStream_t s = (hipStream_t)stream;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W) && aligned16(x) && aligned16(gamma) &&
+        (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, 2);
+        if (gp.kind == 1 || gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, x, act_scale, smooth_inv, Y,
+                                   nullptr, 0, 0, 0, 0, M, N, K, g, G, s, resid, gamma, eps,
+                                   resid ? h_out : nullptr));
+            if (!resid && h_out)
+                FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
+            return FA_OK;
+        }
+    }
+    // separate launches: h_out <- x (+ resid), then RMSNorm + quant, then the linear
+    Workspace* ws = nullptr;
+    rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->xq;
+    rc = grow(&p, &ws->xq_bytes, nk, s);
+    ws->xq = (int8_t*)p;
+    if (rc) return rc;
+    p = ws->xs;
+    rc = grow(&p, &ws->xs_bytes, (size_t)N * (size_t)G * sizeof(float), s);
+    ws->xs = (float*)p;
+    if (rc) return rc;
+    uint16_t* h = const_cast<uint16_t*>(x);   // written only when resid is set
+    if (h_out) {
+        FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
+        h = h_out;
+    }
+    FA_HIP(fa::launch_rms_norm_quant(h, resid, gamma, eps, smooth_inv, act_scale, g, G, ws->xq,
+                                     ws->xs, nullptr, N, K, s));
+    return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
+                            s);
+}
+
+int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_size,
+                        const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
+                        const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
+                        uint16_t* act, int F, int N, int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_swiglu";
+    g_err.clear();
+    int rc = check_dims(fn, F, N, K);
+    if (rc) return rc;
+    if (F == 0 || N == 0) return FA_OK;
+    if (F > (1 << 29)) return fail(FA_ERR_INVALID_ARG, "%s: F=%d too large", fn, F);
+    if (!W13 || !w13_scale || !x || !act)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (!gamma && (resid || h_out))
+        return fail(FA_ERR_INVALID_ARG, "%s: resid / h_out need the RMSNorm (gamma)", fn);
+    if (resid && !h_out)
+        return fail(FA_ERR_INVALID_ARG, "%s: a residual addend needs h_out", fn);
+    const size_t nk = (size_t)N * (size_t)K;
+    if (h_out && (overlaps(h_out, nk, x, nk) || overlaps(h_out, nk, resid, nk)))
+        return fail(FA_ERR_INVALID_ARG, "%s: h_out overlaps x or resid", fn);
+    if (gamma && K > 65536) return fail(FA_ERR_INVALID_ARG, "%s: K=%d exceeds 65536", fn, K);
+    hipStream_t s = (hipStream_t)stream;
+    const int M = 2 * F;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W13) && aligned16(x) && (!gamma || aligned16(gamma)) &&
+        (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, gamma ? 2 : 0, 1);
+        if (gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W13, w13_scale, nullptr, nullptr, x, act_scale, smooth_inv,
+                                   act, nullptr, 0, 0, 0, 0, M, N, K, g, G, s, resid, gamma, eps,
+                                   resid ? h_out : nullptr));
+            if (!resid && h_out)
+                FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
+            return FA_OK;
+        }
+    }
+    // separate launches: the linear into scratch [N, 2F], then the pairs
+    Workspace* ws = nullptr;
+    rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->yt;
+    rc = grow(&p, &ws->yt_bytes, (size_t)N * (size_t)M * 2, s);
+    ws->yt = (uint16_t*)p;
+    if (rc) return rc;
+    uint16_t* yt = ws->yt;
+    rc = gamma ? fa_w8a8_gemm_rms(W13, w13_scale, group_size, act_scale, smooth_inv, x, resid,
+                                  h_out, gamma, eps, yt, M, N, K, stream)
+               : fa_w8a8_gemm(W13, w13_scale, group_size, act_scale, smooth_inv, x, yt, M, N, K,
+                              stream);
+    if (rc) return rc;
+    FA_HIP(fa::launch_swiglu_pairs(yt, act, (int64_t)N * F, s));
+    return FA_OK;
+}
+
+int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_size,
+                          const uint16_t* act_scale, const uint16_t* smooth_inv,
+                          const uint16_t* gate, const uint16_t* up, uint16_t* Y, int M, int N,
+                          int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_silu_mul";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !gate || !up || !Y)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    hipStream_t s = (hipStream_t)stream;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W) && aligned16(gate) && aligned16(up)) {
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, 1);
+        if (gp.kind == 1 || gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, gate, act_scale, smooth_inv,
+                                   Y, nullptr, 0, 0, 0, 0, M, N, K, g, G, s, up));
+            return FA_OK;
+        }
+    }
+    Workspace* ws = nullptr;
+    rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->xq;
+    rc = grow(&p, &ws->xq_bytes, (size_t)N * (size_t)K, s);
+    ws->xq = (int8_t*)p;
+    if (rc) return rc;
+    p = ws->xs;
+    rc = grow(&p, &ws->xs_bytes, (size_t)N * (size_t)G * sizeof(float), s);
+    ws->xs = (float*)p;
+    if (rc) return rc;
+    FA_HIP(fa::launch_quantize_activations(gate, up, fa::Prologue::kSiluMul, act_scale, smooth_inv,
                                            ws->xq, ws->xs, nullptr, N, K, g, G, s));
     return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             s);

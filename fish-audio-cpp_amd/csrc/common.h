@@ -52,6 +52,42 @@ __device__ __forceinline__ float subgroup_max(float v) {
     return v;
 }
 
+// DPP move of a float within 16-lane rows (bound_ctrl off: lanes with no
+// source read 0).
+template <int CTL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
+}
+
+// The shuffle-down sum tree of a 32-lane CUDA warp (offsets 16, 8, 4, 2, 1,
+// `v += __shfl_down(v, off)`), on each 32-lane half of the wave.  Lane 0 of
+// each half gets exactly the reference's pairing (rms_norm.cu:29-41): the
+// cross-row step is a shuffle, the in-row steps are DPP row_shl (lane i reads
+// lane i + off; lanes past the row end read 0, and their sums are never used).
+__device__ __forceinline__ float warp32_sum_down(float v) {
+    v += __shfl_down(v, 16, 32);
+    v += dpp_f<0x108>(v);   // row_shl:8
+    v += dpp_f<0x104>(v);   // row_shl:4
+    v += dpp_f<0x102>(v);   // row_shl:2
+    v += dpp_f<0x101>(v);   // row_shl:1
+    return v;
+}
+
+// Reference SiLU (src/kernels/ffn_activations.cu:15) with expf replaced by a
+// double-precision exp rounded to float; the division is IEEE.
+__device__ __forceinline__ float silu_f(float v) {
+    float e = (float)exp(-(double)v);
+    return v / (1.0f + e);
+}
+
+// RMSNorm scale 1/sqrt(sum_sq / dim + eps) (rms_norm.cu:44), rsqrtf replaced
+// by a double-precision 1/sqrt rounded to float.
+__device__ __forceinline__ float rms_inv(float sum_sq, int dim, float eps) {
+    const float t = sum_sq / (float)dim + eps;
+    return (float)(1.0 / sqrt((double)t));
+}
+
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace fa
@@ -81,6 +117,9 @@ hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint1
 hipError_t launch_elementwise(int op, uint16_t* a, const uint16_t* b, int64_t n,
                               hipStream_t stream);
 
+// act[i] = fp16(fp16(silu(y[2i])) * y[2i + 1]) for i < n (interleaved pairs).
+hipError_t launch_swiglu_pairs(const uint16_t* y, uint16_t* act, int64_t n, hipStream_t stream);
+
 hipError_t launch_quantize_weights(const uint16_t* w, int64_t rows, int64_t K, int g,
                                    int8_t* q, uint16_t* scale, hipStream_t stream);
 
@@ -95,23 +134,35 @@ struct GemvPlan {
     int spg = 0;     // mfma: 64-byte K steps per group
     int maxg = 0;    // mfma: groups per wave
     bool lc = false; // mfma: all terms in LDS, one chain lane per output
+    int pro = 0;     // dot with in-kernel quantization: fused prologue (0 plain,
+                     // 1 SiLU*mul, 2 residual + RMSNorm)
+    int epi = 0;     // dot: 1 = SwiGLU pair epilogue (rows interleaved w1 / w3)
     int grid = 0, block = 0;
     size_t lds = 0;
 };
-// qx: the dot kernel quantizes the fp16 token itself (N == 1 only).
-GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx);
+// qx: the dot kernel quantizes the fp16 token itself (N == 1 only); pro != 0
+// adds a fused prologue in front of that quantizer (N == 1, K <= 12288,
+// K % 8 == 0), else the plan is empty.
+// epi == 1 plans the SwiGLU pair epilogue (two rows per wave, M even,
+// pro 0 or 2): Y [M / 2] gets fp16(fp16(silu(row 2i)) * row 2i+1).
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
 // [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to
 // dbg_partials[((tok - dbg_tok0) * dbg_rows + (row - dbg_row0)) * G + group].
 // With X non-null (dot kernel only) the kernel quantizes the fp16 token X
 // itself (act_scale / smooth_inv as in launch_quantize_activations) and
-// ignores x_q / x_scale.
+// ignores x_q / x_scale.  With p.pro == 1, X is the gate and x2 the up
+// projection (SiLU * mul first); with p.pro == 2, X is the residual stream, x2
+// the residual addend (nullable), gamma / eps the RMSNorm, and h_out
+// (nullable; must not overlap X or x2) receives fp16(X + x2).
 hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
                        const int8_t* x_q, const float* x_scale, const uint16_t* X,
                        const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
                        int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
-                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream);
+                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream,
+                       const uint16_t* x2 = nullptr, const uint16_t* gamma = nullptr,
+                       float eps = 0.0f, uint16_t* h_out = nullptr);
 
 // Prefill GEMM on int8 MFMA with LDS-staged tiles.
 hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,

@@ -1,520 +1,12 @@
-// gemv.hip -- decode-shaped W8A8 linear (N <= 16 tokens) for CDNA4.
-//
-// Replaces the reference's int8_matvec_dequant_kernel (N == 1), its
-// small-batch kernel (2 <= N <= 4) and, for 5 <= N <= 16, its per-group
-// cuBLAS loop (src/kernels/int8_gemm.cu:245-380, 439-498).
-//
-// Both kernels below form every int32 per-group partial P_g exactly and then
-// sum the groups in the reference accumulate kernel's order
-// (int8_gemm.cu:213-234, nvcc contracting `acc += float(P) * ws * xs` into
-// fma(float(P) * ws, xs, acc)), sequentially over g = 0, 1, ..., so the fp16
-// output is bit-identical to the host oracle.  Splitting K across waves only
-// changes who computes the terms float(P_g) * ws; the fma chain over the terms
-// runs in group order on one lane per output.
-//
-// gemv_dot_kernel (N == 1): one wave streams R = 1 or 2 weight rows.  A row's
-// 64/R lanes each load 16 bytes per pass (128-bit loads, a pass covers
-// 1024/R contiguous bytes of the row) and form 4 v_dot4_i32_i8 products with
-// the activation bytes; lanes holding the same K-group (g/16 of them) add
-// their partials with cross-lane shuffles.  Up to KD passes are in flight per
-// wave (a register ring refilled as it drains); no split-K, so every CU keeps
-// dozens of independent row streams.
-//
-// gemv_mfma_kernel (2 <= N <= 16): a workgroup owns 16 weight rows; its NW
-// waves split the K-groups into contiguous ranges.  Lane l streams 16 bytes of
-// row l&15 at byte offset 16*(l>>4) of each 64-byte K step, the tokens' int8
-// activations ride in the second MFMA operand with the same byte mapping, so
-// v_mfma_i32_16x16x64_i8 yields the exact int32 dot of every (row, token) pair
-// over 64 bytes; g/64 chained MFMAs make P_g.  Terms are kept in registers;
-// afterwards the waves pass the running fp32 sums along in group order
-// through LDS.
-#include "common.h"
+// gemv.hip -- decode-shaped W8A8 linear (N <= 16 tokens): plan, launch and
+// the instantiations of the small-batch MFMA kernel.  The kernels and the
+// design notes are in gemv_kernels.h; the N == 1 kernel families are
+// instantiated in gemv_dot*.hip.
+#include "gemv_kernels.h"
 
 namespace fa {
+using namespace gv;
 namespace {
-
-struct DbgWindow {
-    int32_t* p;
-    int row0, rows, tok0, toks;
-    __device__ bool in(int row, int tok) const {
-        return p && row >= row0 && row < row0 + rows && tok >= tok0 && tok < tok0 + toks;
-    }
-    __device__ int32_t& at(int row, int tok, int gi, int G) const {
-        return p[((size_t)(tok - tok0) * rows + (row - row0)) * G + gi];
-    }
-};
-
-__device__ __forceinline__ v4i ld16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
-
-// ------------------------------------------------------------ N == 1 ----
-
-constexpr int kDotWaves = 4;     // waves per workgroup, staged int8 codes
-constexpr int kDotWavesQx = 8;   // waves per workgroup, in-kernel quantization
-
-// Sum of an int over aligned blocks of LG lanes (all lanes get the block sum).
-// LG <= 16 stays inside a 16-lane DPP row: quad_perm swaps, then half-row and
-// row mirrors, one v_add_*_dpp each.  Integer sums are exact in any order.
-template <int LG>
-__device__ __forceinline__ int group_sum(int p, int lg_rt) {
-    if constexpr (LG == 0) {
-        for (int off = 1; off < (1 << lg_rt); off <<= 1) p += __shfl_xor(p, off, 64);
-        return p;
-    } else {
-        if constexpr (LG >= 2) p += __builtin_amdgcn_update_dpp(0, p, 0xB1, 0xF, 0xF, false);
-        if constexpr (LG >= 4) p += __builtin_amdgcn_update_dpp(0, p, 0x4E, 0xF, 0xF, false);
-        if constexpr (LG >= 8) p += __builtin_amdgcn_update_dpp(0, p, 0x141, 0xF, 0xF, false);
-        if constexpr (LG >= 16) p += __builtin_amdgcn_update_dpp(0, p, 0x140, 0xF, 0xF, false);
-        if constexpr (LG >= 32) p += __shfl_xor(p, 16, 64);
-        if constexpr (LG >= 64) p += __shfl_xor(p, 32, 64);
-        return p;
-    }
-}
-
-// Max of a non-negative float over aligned blocks of 2^lgl lanes (runtime
-// width; all lanes get the block max).  Within 16-lane DPP rows one
-// v_max_f32_dpp per step; wider blocks add xor shuffles across rows.  The
-// max is exact in any order.
-template <int CTL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float block_max(float m, int lgl) {
-    if (lgl >= 1) m = fmaxf(m, dpp_f<0xB1>(m));    // quad_perm [1,0,3,2]
-    if (lgl >= 2) m = fmaxf(m, dpp_f<0x4E>(m));    // quad_perm [2,3,0,1]
-    if (lgl >= 3) m = fmaxf(m, dpp_f<0x141>(m));   // row_half_mirror
-    if (lgl >= 4) m = fmaxf(m, dpp_f<0x140>(m));   // row_mirror
-    if (lgl >= 5) m = fmaxf(m, __shfl_xor(m, 16, 64));
-    if (lgl >= 6) m = fmaxf(m, __shfl_xor(m, 32, 64));
-    return m;
-}
-
-// One wave streams R rows (R = 1, 2 or 4; 64/R lanes per row, 16 bytes per
-// lane per pass).  After 4 v_dot4 per lane, lanes of one K-group (LG = g/16
-// of them) sum their partials with DPP, so every lane of a group holds the
-// exact int32 P_g.  The groups of a pass are then in known lanes: group slot j
-// of row r sits in lane r * 64/R + j * LG.  Each of those terms
-// float(P_g) * ws is broadcast with v_readlane, and every lane advances its
-// rows' fp32 sums in group order, acc = fma(term, x_scale[g], acc) -- the
-// reference's accumulate order (int8_gemm.cu:231), so the result is the
-// oracle's bit for bit without any per-row serial tail.
-//
-// QX: the kernel quantizes the fp16 token itself (int8_gemm.cu:147-211
-// semantics: per-group amax/127 or a static scale, optional smooth_inv) while
-// the first weight loads are in flight; otherwise it stages the given int8
-// activations and fp32 scales.  Either way x_q [K] and x_scale [G] sit in LDS.
-//
-// Work: row blocks of NWV * R rows (NWV waves per workgroup); block b,
-// b + gridDim.x, ... belong to workgroup b.  A uniform cursor (row block,
-// pass) walks the wave's passes in order and the weight ring is KD passes
-// ahead of the consumer.  g is a power of two (lg_g = log2 g) with
-// 16 <= g <= 16 * 64/R.  With QX every workgroup quantizes the whole token,
-// so QX launches use 8-wave workgroups (half as many copies of that work).
-template <int R, int KD, int LG, bool QX, int XV, int NWV = kDotWaves, int kAb = 0>
-__global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
-    const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
-    const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
-    const uint16_t* __restrict__ X, const uint16_t* __restrict__ act_scale,
-    const uint16_t* __restrict__ smooth_inv,
-    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int K, int lg_g, int G, int passes,
-    int nblocks) {
-    constexpr int RL = 64 / R;            // lanes per row
-    constexpr int PB = RL * 16;           // bytes of a row per pass
-    constexpr int GPP = RL / LG;          // groups per row per pass
-    constexpr int NT = NWV * 64;
-    static_assert(LG >= 1 && LG <= RL, "group must fit a row's lanes");
-    extern __shared__ __align__(16) float lds[];
-    const int Kp = (K + 15) & ~15;
-    int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                  // [Kp]
-    float* xs_s = lds + Kp / 4;                                      // [G], padded to 4
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-
-    const int rsub = lane / RL;
-    const int li = lane % RL;
-    const int lane_k = li * 16;
-
-    // ---- activation loads first: their wait then does not cover the ring.
-    // XV 16-byte chunks per thread (int8 codes, or 8 fp16 values with QX);
-    // unconditional loads from clamped addresses (a load under a branch makes
-    // the compiler wait for it on the spot).
-    v4i xr[XV];
-    float xsr = 0.0f;
-    if constexpr (!QX) {
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int k = (tid + i * NT) * 16;
-            xr[i] = ld16(x_q + (k < Kp ? k : Kp - 16));
-        }
-        xsr = x_scale[tid < G ? tid : G - 1];
-    } else {
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int k = (tid + i * NT) * 8;
-            xr[i] = *reinterpret_cast<const v4i*>(X + (k < K ? k : K - 8));
-        }
-    }
-
-    // ---- weight ring
-    int l_blk = blockIdx.x, l_pass = 0;     // load cursor (uniform)
-    const int8_t* const wlast = W + (size_t)(M - 1) * K;
-    v4i a[KD];
-    uint16_t sc[KD];
-    const v4i zero = {0, 0, 0, 0};
-    auto row_of_blk = [&](int blk) { return (blk * NWV + wave) * R + rsub; };
-    auto load = [&](int slot) {
-        const bool live = l_blk < nblocks;
-        const int row = row_of_blk(live ? l_blk : blockIdx.x);
-        const int rowc = row < M ? row : M - 1;
-        const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
-        const int k = l_pass * PB + lane_k;
-        const bool ok = live && k < K;
-        const int kk = ok ? k : 0;
-        // no select on the loaded value (that would wait for the load here):
-        // bytes past K meet zero activations in consume()
-        const v4i wa = ld16(wrow + kk);
-        if constexpr ((kAb & 2) == 0)
-            sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
-        else
-            sc[slot] = (uint16_t)kk;
-        a[slot] = wa;
-        if (++l_pass == passes) {
-            l_pass = 0;
-            l_blk += gridDim.x;
-        }
-    };
-#pragma unroll
-    for (int s = 0; s < KD; ++s) load(s);
-
-    // ---- stage activations into LDS
-    if constexpr ((kAb & 1) != 0) {
-    } else if constexpr (!QX) {
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int k = (tid + i * NT) * 16;
-            if (k < Kp) *reinterpret_cast<v4i*>(xq_s + k) = xr[i];
-        }
-        if (tid < G) xs_s[tid] = xsr;
-        for (int k = (tid + XV * NT) * 16; k < Kp; k += NT * 16)   // K > 16 KB
-            *reinterpret_cast<v4i*>(xq_s + k) = ld16(x_q + k);
-        for (int i = tid + NT; i < G; i += NT) xs_s[i] = x_scale[i];
-    } else {
-        // Chunk c holds x[8c, 8c + 8); chunk c of thread tid is tid + i * NT,
-        // so a K-group (g / 8 chunks) lies in g / 8 consecutive lanes of one
-        // wave.  Its |v| maximum (exact in any order) comes from xor
-        // shuffles, then scale and int8 codes are formed in registers: no
-        // atomics and a single barrier before the codes are read.
-        const int glanes = 1 << (lg_g - 3);
-        auto chunk = [&](int c, const v4i& raw) {
-            const int k = c * 8;
-            const bool ok = k < K;
-            const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                v[e] = h2f(h[e]);
-                if (smooth_inv) v[e] *= h2f(smooth_inv[ok ? k + e : e]);
-            }
-            const int gi = ok ? k >> lg_g : G - 1;
-            float sc_;
-            if (act_scale) {
-                sc_ = h2f(act_scale[gi]);
-                sc_ = sc_ < 1e-8f ? 1e-8f : sc_;
-            } else {
-                float m = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-                if (!ok) m = 0.0f;
-                m = block_max(m, lg_g - 3);
-                sc_ = act_scale_from_amax(m);
-            }
-            if (ok) {
-                const float inv = 1.0f / sc_;
-                int q[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
-                uint2 u;
-                u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                      ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
-                u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
-                      ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
-                *reinterpret_cast<uint2*>(xq_s + k) = u;
-                if ((c & (glanes - 1)) == 0) xs_s[gi] = sc_;
-            }
-        };
-#pragma unroll
-        for (int i = 0; i < XV; ++i) chunk(tid + i * NT, xr[i]);
-        for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
-            const int c = c0 + tid;
-            chunk(c, *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8)));
-        }
-    }
-    if constexpr ((kAb & 1) == 0) __syncthreads();
-
-    // ---- consume
-    int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    auto consume = [&](int slot) {
-        const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
-        const int k = kbase + lane_k;
-        v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
-        if (k >= K) b = zero;
-        int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
-        p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
-        p = __builtin_amdgcn_sdot4(a[slot].z, b.z, p, false);
-        p = __builtin_amdgcn_sdot4(a[slot].w, b.w, p, false);
-        p = group_sum<LG>(p, 0);
-        const float term = (float)p * h2f(sc[slot]);
-        if (dbg.p) {
-            const int row = row_of_blk(c_blk);
-            if (k < K && (li & (LG - 1)) == 0 && row < M && dbg.in(row, 0))
-                dbg.at(row, 0, k >> lg_g, G) = p;
-        }
-        if constexpr ((kAb & 4) != 0) {
-            acc[0] += term;
-        } else {
-            // group order within the pass: slot j of every row; the pass's
-            // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
-            float xsv[GPP];
-            const float* xp = xs_s + (kbase >> lg_g);
-            if constexpr (GPP == 4) {
-                const float4 v = *reinterpret_cast<const float4*>(xp);
-                xsv[0] = v.x; xsv[1] = v.y; xsv[2] = v.z; xsv[3] = v.w;
-            } else if constexpr (GPP == 2) {
-                const float2 v = *reinterpret_cast<const float2*>(xp);
-                xsv[0] = v.x; xsv[1] = v.y;
-            } else {
-#pragma unroll
-                for (int j = 0; j < GPP; ++j) xsv[j] = xp[j];
-            }
-#pragma unroll
-            for (int j = 0; j < GPP; ++j) {
-                const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
-                if (kg < K) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const float tj = __builtin_bit_cast(
-                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
-                                                             r * RL + j * LG));
-                        acc[r] = __builtin_fmaf(tj, xsv[j], acc[r]);
-                    }
-                }
-            }
-        }
-        if (++c_pass == passes) {
-            const int row = row_of_blk(c_blk);
-            // lane r*RL (li == 0) of row slot r stores that row
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (rsub == r && li == 0 && row < M) Y[row] = f2h(acc[r]);
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-            c_pass = 0;
-            c_blk += gridDim.x;
-        }
-    };
-    // Rounds that refill the ring, then a last round that only drains it (so
-    // every load is unconditional and the wait counts stay exact).
-    const int my_blocks = (nblocks - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-    const int items = my_blocks * passes;
-    int base = 0;
-    for (; base + KD < items; base += KD) {
-#pragma unroll
-        for (int s = 0; s < KD; ++s) {
-            consume(s);
-            load(s);
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < KD; ++s)
-        if (base + s < items) consume(s);
-}
-
-// ------------------------------------------------------ 2 <= N <= 16 ----
-
-constexpr int kTile = 16;
-
-template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0, int kKD = 12>
-__global__ __launch_bounds__(512) void gemv_mfma_kernel(
-    const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
-    const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
-    uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G) {
-    constexpr int NSTEP = SPG * MAXG;
-    // ring depth: kKD steps, 8 when 16+ groups' terms are held in registers
-    constexpr int KDM = (!LC && MAXG >= 16) ? 8 : kKD;
-    constexpr int KD = NSTEP < KDM ? NSTEP : KDM;
-    extern __shared__ float lds[];
-    float* ws_s = lds;                   // [16 rows][G]
-    float* xs_s = lds + kTile * G;       // [16 tokens][G]
-    float* chain = lds + 2 * kTile * G;  // [16 tokens][16 rows] (!LC)
-    // LC: every term float(P_g) * ws in LDS, [G][ns tokens][16 rows]
-    const int ns = N <= 8 ? 8 : 16;
-    float* tl = lds + 2 * kTile * G;
-
-    const int NW = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int row0 = blockIdx.x * kTile;
-    const int gb = (wave * G) / NW;
-    const int ng = ((wave + 1) * G) / NW - gb;
-    const int nsteps = ng * SPG;
-
-    const int lr = lane & 15;            // A: weight row in tile; B: token
-    const int kq = (lane >> 4) * 16;
-    const int row_ld = min(row0 + lr, M - 1);
-    const size_t kbase = (size_t)gb * SPG * 64 + kq;
-    const int8_t* wp = W + (size_t)row_ld * K + kbase;
-    // token lanes past N read token N-1: their MFMA columns are never stored
-    const int8_t* xp = x_q + (size_t)min(lr, N - 1) * K + kbase;
-
-    v4i a[KD], b[KD];
-    const v4i zero = {0, 0, 0, 0};
-    // unconditional loads, no select on the loaded data: a select would make
-    // the compiler wait for each load right where it is issued
-    auto load = [&](int slot, int step) {
-        const size_t off = (size_t)(step < nsteps ? step : 0) * 64;
-        a[slot] = ld16(wp + off);
-        if constexpr ((kAb & 1) == 0) b[slot] = ld16(xp + off);
-        else b[slot] = a[slot];
-    };
-    // Scales of the tile's 16 rows and of the tokens, all groups: at most 5
-    // per thread (the plan keeps G <= 20 * NW).  Their loads go out before
-    // the weight ring's, so the wait before the LDS stores covers only them.
-    // Token rows past N repeat token N-1 (their outputs are never stored).
-    constexpr int kSt = 5;
-    uint16_t wsr[kSt];
-    float xsr[kSt];
-#pragma unroll
-    for (int q = 0; q < kSt; ++q) {
-        const int i = min((int)threadIdx.x + q * (int)blockDim.x, kTile * G - 1);
-        const int r = i / G, gi = i - r * G;
-        const int row = min(row0 + r, M - 1);
-        wsr[q] = w_scale[G == 1 ? (size_t)row : (size_t)row * G + gi];
-        xsr[q] = x_scale[(size_t)min(r, N - 1) * G + gi];
-    }
-#pragma unroll
-    for (int s = 0; s < KD; ++s) load(s, s);
-#pragma unroll
-    for (int q = 0; q < kSt; ++q) {
-        const int i = threadIdx.x + q * blockDim.x;
-        if ((kAb & 4) == 0 && i < kTile * G) {
-            ws_s[i] = h2f(wsr[q]);
-            xs_s[i] = xsr[q];
-        }
-    }
-    __syncthreads();
-
-    const int orow = 4 * (lane >> 4);    // this lane's 4 output rows: orow .. orow+3
-    float terms[LC ? 1 : MAXG][4];
-#pragma unroll
-    for (int j = 0; j < MAXG; ++j) {
-        v4i P = zero;
-#pragma unroll
-        for (int s = 0; s < SPG; ++s) {
-            const int step = j * SPG + s;
-            const int slot = step % KD;
-            P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], b[slot], P, 0, 0, 0);
-            load(slot, step + KD);
-        }
-        const int gi = gb + (j < ng ? j : 0);
-        if constexpr (LC) {
-            if (j < ng && lr < ns) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    tl[(gi * ns + lr) * kTile + orow + r] = (float)P[r] * ws_s[(orow + r) * G + gi];
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) terms[j][r] = (float)P[r] * ws_s[(orow + r) * G + gi];
-        }
-        if constexpr (kDbg) {
-            if (j < ng && lr < N) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = row0 + orow + r;
-                    if (row < M && dbg.in(row, lr)) dbg.at(row, lr, gb + j, G) = P[r];
-                }
-            }
-        }
-    }
-
-    if constexpr (LC) {
-        // one lane per output runs the whole chain in group order
-        __syncthreads();
-        for (int t = threadIdx.x; t < kTile * N; t += blockDim.x) {
-            const int r = t & (kTile - 1), tok = t >> 4;
-            float acc = 0.0f;
-            for (int gi = 0; gi < G; ++gi)
-                acc = __builtin_fmaf(tl[(gi * ns + tok) * kTile + r], xs_s[tok * G + gi], acc);
-            if (row0 + r < M) Y[(size_t)tok * M + row0 + r] = f2h(acc);
-        }
-    } else {
-        // this lane's token scales for the wave's groups, read before the chain
-        // (the chain's LDS writes would otherwise keep these reads inside it)
-        float xsv[MAXG];
-#pragma unroll
-        for (int j = 0; j < MAXG; ++j) xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
-
-        // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
-        // the previous wave's sums over its own groups.
-        for (int w = 0; w < NW; ++w) {
-            if (wave == w) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float acc = w == 0 ? 0.0f : chain[lr * kTile + orow + r];
-#pragma unroll
-                    for (int j = 0; j < MAXG; ++j)
-                        if (j < ng) acc = __builtin_fmaf(terms[j][r], xsv[j], acc);
-                    chain[lr * kTile + orow + r] = acc;
-                }
-            }
-            __syncthreads();
-        }
-        for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
-            const int t = i / kTile, r = i - t * kTile;
-            if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
-        }
-    }
-}
-
-// Host-side instantiation tables.
-using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*,
-                       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,
-                       int, int, int, int, int, int);
-
-template <int R, int KD, bool QX, int XV, int NWV>
-DotFn dot_for_lg(int lg) {
-    switch (lg) {
-        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, NWV>;     // g64
-        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, NWV>;     // g128
-        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, NWV>;    // g256
-        default: return gemv_dot_kernel<R, KD, 32, QX, XV, NWV>;   // g512
-    }
-}
-
-template <int R, bool QX, int XV, int NWV>
-DotFn dot_for_kd(int kd, int lg) {
-    switch (kd) {
-        case 3: return dot_for_lg<R, 3, QX, XV, NWV>(lg);
-        case 4: return dot_for_lg<R, 4, QX, XV, NWV>(lg);
-        default: return dot_for_lg<R, 5, QX, XV, NWV>(lg);
-    }
-}
-
-// Staged int8 codes: 4 waves, XV = 1 or 3 16-byte chunks per thread
-// (K <= 4096 / 12288).  In-kernel quantization: 8 waves, XV = 1 or 3 chunks of
-// 8 fp16 values per thread (K <= 4096 / 12288).  Larger K use a tail loop.
-template <int R>
-DotFn dot_for(bool qx, int K, int kd, int lg) {
-    if (qx)
-        return K <= 4096 ? dot_for_kd<R, true, 1, kDotWavesQx>(kd, lg)
-                         : dot_for_kd<R, true, 3, kDotWavesQx>(kd, lg);
-    return K <= 4096 ? dot_for_kd<R, false, 1, kDotWaves>(kd, lg)
-                     : dot_for_kd<R, false, 3, kDotWaves>(kd, lg);
-}
 
 template <bool D>
 using MfmaFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*, uint16_t*,
@@ -559,11 +51,15 @@ int round_maxg(int m) {
 
 }  // namespace
 
-GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx) {
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi) {
     GemvPlan p{};
+    if (pro != 0 && (!qx || N != 1 || K > 3 * 8 * 64 * kDotWavesQx || K % 8 != 0)) return p;
+    if (epi != 0 && (!qx || N != 1 || pro == 1 || (M & 1))) return p;
     if (N == 1 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 16 == 0 && K <= 32768) {
         const int lgroups = g / 16;
-        p.kind = (M >= 4096 && lgroups <= 32) ? 2 : 1;   // rows per wave
+        p.kind = ((M >= 4096 || epi) && lgroups <= 32) ? 2 : 1;   // rows per wave
+        if (epi && p.kind != 2) return GemvPlan{};
+        p.epi = epi;
         const int R = p.kind;
         if (lgroups > 64 / R) return GemvPlan{};
         const int PB = (64 / R) * 16;
@@ -576,6 +72,8 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx) {
         p.block = nwv * 64;
         const int Kp = (K + 15) & ~15;
         p.lds = (size_t)Kp + (size_t)((G + 3) & ~3) * sizeof(float);   // xs padded for float4 reads
+        if (pro == 2) p.lds += (size_t)Kp * 2 + 33 * sizeof(float);      // fp16 row, warp sums
+        p.pro = pro;
         if (g < 16) return GemvPlan{};
         if (p.lds > 64 * 1024) return GemvPlan{};
         int lg = 0;
@@ -614,19 +112,25 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
                        const int8_t* x_q, const float* x_scale, const uint16_t* X,
                        const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
                        int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
-                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream) {
+                       int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream,
+                       const uint16_t* x2, const uint16_t* gamma, float eps, uint16_t* h_out) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
+    const ProArgs pro{x2, gamma, h_out, eps};
     if (p.kind == 1 || p.kind == 2) {
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)
         if (qx != (p.block == kDotWavesQx * 64)) return hipErrorInvalidValue;   // planned for the other input
-        DotFn fn = p.kind == 1 ? dot_for<1>(qx, K, p.kd, lgl) : dot_for<2>(qx, K, p.kd, lgl);
+        if (p.pro == 2 && !gamma) return hipErrorInvalidValue;
+        if (p.epi && (p.kind != 2 || !qx || (M & 1))) return hipErrorInvalidValue;
+        DotFn fn = p.epi ? dot_swiglu(p.pro, K, p.kd, lgl)
+                 : p.pro ? dot_pro(p.kind, p.pro, K, p.kd, lgl)
+                         : dot_plain(p.kind, qx, K, p.kd, lgl);
         // one workgroup per row block (the cursor also serves a smaller grid)
         const int grid = p.grid;
         hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,
-                           X, act_scale, smooth_inv, Y, dbg, M, K, p.lg, G, p.passes, p.grid);
+                           X, act_scale, smooth_inv, Y, dbg, M, K, p.lg, G, p.passes, p.grid, pro);
     } else if (p.kind == 3) {
-        if (X) return hipErrorInvalidValue;
+        if (X || p.pro) return hipErrorInvalidValue;
         const bool d = dbg_partials != nullptr;
         if (d)
             hipLaunchKernelGGL(mfma_for<true>(p.lc, p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,

@@ -13,12 +13,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Reference SiLU (src/kernels/ffn_activations.cu:15) with expf replaced by a
-// double-precision exp rounded to float; the division is IEEE.
-__device__ __forceinline__ float silu_f(float v) {
-    float e = (float)exp(-(double)v);
-    return v / (1.0f + e);
-}
 
 // Load VEC consecutive fp16 values (16-byte load when VEC == 8).
 template <int VEC>
@@ -63,11 +57,6 @@ __device__ __forceinline__ void store_h(uint16_t* p, const uint16_t (&h)[VEC]) {
     }
 }
 
-template <int CTL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
-}
 
 // Runtime-width subgroup max (width = 1 << lg, lg <= 6; all lanes get it);
 // every lane of the wave must call it.  Within 16-lane rows one DPP op per
@@ -82,19 +71,6 @@ __device__ __forceinline__ float subgroup_max_rt(float v, int lg) {
     return v;
 }
 
-// The shuffle-down sum tree of a 32-lane CUDA warp (offsets 16, 8, 4, 2, 1,
-// `v += __shfl_down(v, off)`), on each 32-lane half of the wave.  Lane 0 of
-// each half gets exactly the reference's pairing: the cross-row step is a
-// shuffle, the in-row steps are DPP row_shl (lane i reads lane i + off;
-// lanes past the row end read 0, and their sums are never used).
-__device__ __forceinline__ float warp32_sum_down(float v) {
-    v += __shfl_down(v, 16, 32);
-    v += dpp_f<0x108>(v);   // row_shl:8
-    v += dpp_f<0x104>(v);   // row_shl:4
-    v += dpp_f<0x102>(v);   // row_shl:2
-    v += dpp_f<0x101>(v);   // row_shl:1
-    return v;
-}
 
 // Values entering the quantizer for elements [k, k+VEC) of token row `n`:
 // the prologue output rounded to fp16 (what the reference writes to memory
@@ -292,8 +268,7 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
         float v = tid < nw ? s_warp[tid] : 0.0f;
         v = warp32_sum_down(v);
         if (tid == 0) {
-            float t = v / (float)dim + eps;
-            s_rms = (float)(1.0 / sqrt((double)t));
+            s_rms = rms_inv(v, dim, eps);
         }
     }
     __syncthreads();
@@ -380,6 +355,16 @@ __global__ __launch_bounds__(kThreads) void elementwise_kernel(int op, uint16_t*
         else r = va + h2f(b[i]);
         a[i] = f2h(r);
     }
+}
+
+// SwiGLU on interleaved pairs: act[i] = fp16(fp16(silu(y[2i])) * y[2i + 1])
+// (silu_forward then mul_forward, ffn_activations.cu:12-17, 35-39).
+__global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const uint16_t* __restrict__ y,
+                                                                uint16_t* __restrict__ act,
+                                                                int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+        act[i] = f2h(h2f(f2h(silu_f(h2f(y[2 * i])))) * h2f(y[2 * i + 1]));
 }
 
 // ------------------------------------------------------ weight quantizer ----
@@ -485,6 +470,15 @@ hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint1
     hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(n_tokens), dim3(block), lds, stream, x, resid,
                        weight, eps, smooth_inv, act_scale, x_q, x_scale, out_f16, dim, T, g, G, lg,
                        vec8 ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_pairs(const uint16_t* y, uint16_t* act, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    int64_t blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(swiglu_pairs_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, y,
+                       act, n);
     return hipGetLastError();
 }
 

@@ -29,7 +29,8 @@ HIP_FLAGS = [
     "-Wall",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemv.hip", "gemm.hip"]
+HIP_SOURCES = ["quant.hip", "gemv.hip", "gemv_dot.hip", "gemv_dot_pro.hip", "gemv_dot_swiglu.hip",
+               "gemm.hip"]
 HOST_SOURCES = ["api.cpp", "loader.cpp", "kernels_cxx.cpp"]
 
 
@@ -50,7 +51,7 @@ def build_library(verbose=False):
     inc = ["-I", os.path.join(PKG_ROOT, "include")]
     flags = [f for f in HIP_FLAGS if f != "-shared"]
     jobs = []
-    for src in HIP_SOURCES + HOST_SOURCES:
+    for src in HIP_SOURCES + HOST_SOURCES:   # the shared kernel header is not a unit
         obj = os.path.join(obj_dir, src + ".o")
         lang = [] if src.endswith(".hip") else ["-x", "hip"]
         jobs.append((obj, [HIPCC] + flags + inc + ["-c"] + lang + [os.path.join(CSRC, src), "-o", obj]))

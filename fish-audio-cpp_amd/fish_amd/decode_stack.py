@@ -4,16 +4,19 @@ Mirrors the per-layer call order of DualAREngine::decode_step
 (src/engine/dual_ar_engine.cc:576-648) with attention omitted (the o_proj
 input is the q slice of the qkv output):
 
-    rms_norm+quant -> qkv -> quant -> o -> residual+rms_norm+quant
-    -> gate_up -> silu*mul+quant -> down -> (residual+rms_norm+quant of the
-    next layer; a plain residual after the last)
+    residual + rms_norm + quant -> qkv -> quant -> o -> residual + rms_norm
+    + quant -> gate_up -> silu*mul + quant -> down -> (the next layer's
+    residual; a plain residual add after the last)
 
-Each residual add is fused into the RMSNorm + quant launch that follows it
-(fa_residual_rms_norm_quant), so a layer takes nine launches, two of which
-(the o-input copy and its quantizer) stand in for attention.
+Every prologue and the SwiGLU product are fused into the linears
+(fa_w8a8_gemm_rms, fa_w8a8_gemm, fa_w8a8_gemm_swiglu), so a layer takes four
+launches at one token.
 
-gate_up is w1 and w3 stacked into one [2 * 9728, 2560] weight (exact when the
-two share their input quantization, i.e. no per-weight smooth_inv).
+gate_up is w1 and w3 with rows interleaved (row 2i = w1 row i, row 2i+1 = w3
+row i) into one [2 * 9728, 2560] weight, so one GEMV wave holds both halves of
+an FFN column and its epilogue forms silu(gate) * up directly; exact when the
+two share their input quantization, i.e. no per-weight smooth_inv.
+
 Weights are synthetic (N(0, 0.02) fp16, quantized group-wise on the device).
 Every layer owns its own weights, so a 36-layer pass streams ~3.6 GB and
 never runs out of the 256 MB last-level cache.
@@ -56,6 +59,7 @@ class DecodeStack:
         dev = "cuda"
         self.h = torch.randn((T, HIDDEN), generator=gen, device=dev).half()
         self.h0 = self.h.clone()
+        self.h_alt = torch.empty_like(self.h)
         # activations / scratch, allocated once
         self.x_in = {name: torch.randn((T, K), generator=gen, device=dev).half()
                      for name, (K, _) in LAYER_SHAPES.items()}
@@ -64,8 +68,7 @@ class DecodeStack:
         self.xq = torch.empty((T, FFN), device=dev, dtype=torch.int8)
         self.xs = torch.empty((T, FFN // 64 + 1), device=dev, dtype=torch.float32)
         self.o_in = torch.empty((T, Q_DIM), device=dev, dtype=torch.float16)
-        self.gate = torch.empty((T, FFN), device=dev, dtype=torch.float16)
-        self.up = torch.empty((T, FFN), device=dev, dtype=torch.float16)
+        self.act = torch.empty((T, FFN), device=dev, dtype=torch.float16)
         lib = ops.lib()
         ops.check(lib.fa_workspace_reserve(max(T, 16), 19456, FFN, g, ops._stream()))
 
@@ -91,58 +94,53 @@ class DecodeStack:
 
     # -- the full decode-step linear stack with fused prologues --
     def run_stack(self):
+        """Four launches per layer: every linear forms its own int8 input.
+
+            qkv      fa_w8a8_gemm_rms     h' = h + down_prev; attention_norm(h')
+            o        fa_w8a8_gemm         the q slice of qkv's output (attention omitted)
+            gate_up  fa_w8a8_gemm_swiglu  h'' = h' + o; ffn_norm(h''); silu(gate) * up
+            down     fa_w8a8_gemm         act
+
+        The residual stream ping-pongs between two buffers (a fused residual
+        write must not overwrite the stream other workgroups still read); the
+        result ends in self.h.  Tokens > 1 take the same entry points, which
+        then run their prologue and linear as separate launches."""
         g, T = self.g, self.T
         l_ = ops.lib()
         s = ops._stream()
-        G2560 = (HIDDEN + g - 1) // g
+        cur, nxt = self.h, self.h_alt
+        if T == 1:
+            o_in = self.y["qkv"]            # the q slice is the row's first Q_DIM values
         for li, lay in enumerate(self.layers):
-            # (previous layer's down residual +) attention_norm + quant -> wqkv
-            if li == 0:
-                ops.check(l_.fa_rms_norm_quant(self.h.data_ptr(), lay["attn_norm"].data_ptr(),
-                                               1e-6, None, None, g, self.xq.data_ptr(),
-                                               self.xs.data_ptr(), None, T, HIDDEN, s))
-            else:
-                ops.check(l_.fa_residual_rms_norm_quant(
-                    self.h.data_ptr(), self.y["down"].data_ptr(), lay["attn_norm"].data_ptr(),
-                    1e-6, None, None, g, self.xq.data_ptr(), self.xs.data_ptr(), None, T, HIDDEN,
-                    s))
             L = lay["qkv"]
-            ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
-                                                self.xq.data_ptr(), self.xs.data_ptr(),
-                                                self.y["qkv"].data_ptr(), L.N, T, L.K, s))
-            # attention omitted: o input is the q slice of the qkv output
-            self.o_in.copy_(self.y["qkv"][:, :Q_DIM])
-            ops.check(l_.fa_quantize_activations(self.o_in.data_ptr(), None, None,
-                                                 self.xq.data_ptr(), self.xs.data_ptr(), T, Q_DIM,
-                                                 g, s))
+            resid = None if li == 0 else self.y["down"].data_ptr()
+            ops.check(l_.fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                          cur.data_ptr(), resid,
+                                          None if li == 0 else nxt.data_ptr(),
+                                          lay["attn_norm"].data_ptr(), 1e-6,
+                                          self.y["qkv"].data_ptr(), L.N, T, L.K, s))
+            if li != 0:
+                cur, nxt = nxt, cur
+            if T != 1:
+                self.o_in.copy_(self.y["qkv"][:, :Q_DIM])
+                o_in = self.o_in
             L = lay["o"]
-            ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
-                                                self.xq.data_ptr(), self.xs.data_ptr(),
-                                                self.y["o"].data_ptr(), L.N, T, L.K, s))
-            # o residual + ffn_norm + quant -> w1|w3
-            ops.check(l_.fa_residual_rms_norm_quant(
-                self.h.data_ptr(), self.y["o"].data_ptr(), lay["ffn_norm"].data_ptr(), 1e-6, None,
-                None, g, self.xq.data_ptr(), self.xs.data_ptr(), None, T, HIDDEN, s))
+            ops.check(l_.fa_w8a8_gemm(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                      o_in.data_ptr(), self.y["o"].data_ptr(), L.N, T, L.K, s))
             L = lay["gate_up"]
-            ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
-                                                self.xq.data_ptr(), self.xs.data_ptr(),
-                                                self.y["gate_up"].data_ptr(), L.N, T, L.K, s))
-            if T == 1:
-                gate_p = self.y["gate_up"].data_ptr()
-                up_p = gate_p + 2 * FFN
-            else:
-                self.gate.copy_(self.y["gate_up"][:, :FFN])
-                self.up.copy_(self.y["gate_up"][:, FFN:])
-                gate_p, up_p = self.gate.data_ptr(), self.up.data_ptr()
-            ops.check(l_.fa_silu_mul_quant(gate_p, up_p, None, None, g, self.xq.data_ptr(),
-                                           self.xs.data_ptr(), None, T, FFN, s))
+            ops.check(l_.fa_w8a8_gemm_swiglu(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                             cur.data_ptr(), self.y["o"].data_ptr(),
+                                             nxt.data_ptr(), lay["ffn_norm"].data_ptr(), 1e-6,
+                                             self.act.data_ptr(), L.N // 2, T, L.K, s))
+            cur, nxt = nxt, cur
             L = lay["down"]
-            ops.check(l_.fa_w8a8_gemm_quantized(L.W.data_ptr(), L.scale.data_ptr(), g,
-                                                self.xq.data_ptr(), self.xs.data_ptr(),
-                                                self.y["down"].data_ptr(), L.N, T, L.K, s))
+            ops.check(l_.fa_w8a8_gemm(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                      self.act.data_ptr(), self.y["down"].data_ptr(), L.N, T,
+                                      L.K, s))
         # the last layer's down residual
-        ops.check(l_.fa_residual_add(self.h.data_ptr(), self.y["down"].data_ptr(), T * HIDDEN, s))
-        del G2560
+        ops.check(l_.fa_residual_add(cur.data_ptr(), self.y["down"].data_ptr(), T * HIDDEN, s))
+        if cur is not self.h:
+            self.h.copy_(cur)
 
     def stack_bytes(self):
         """Algorithmic bytes of one stack pass: int8 W + fp16 scales of all

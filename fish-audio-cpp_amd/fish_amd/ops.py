@@ -46,6 +46,56 @@ def w8a8_gemm(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=No
     return Y
 
 
+def w8a8_gemm_rms(W, w_scale, x, gamma, eps, group_size, resid=None, h_out=None,
+                  act_scale=None, smooth_inv=None, out=None):
+    """RMSNorm (after an optional residual add written to h_out) + linear."""
+    _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale"); _need(x, torch.float16, "x")
+    _need(gamma, torch.float16, "gamma"); _need(resid, torch.float16, "resid")
+    _need(h_out, torch.float16, "h_out")
+    M, K = W.shape
+    N = x.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=x.device)
+    check(lib().fa_w8a8_gemm_rms(_ptr(W), _ptr(w_scale), group_size, _ptr(act_scale),
+                                 _ptr(smooth_inv), _ptr(x), _ptr(resid), _ptr(h_out), _ptr(gamma),
+                                 eps, _ptr(Y), M, N, K, _stream()))
+    return Y
+
+
+def w8a8_gemm_swiglu(W13, w13_scale, x, group_size, gamma=None, eps=1e-6, resid=None,
+                     h_out=None, act_scale=None, smooth_inv=None, out=None):
+    """act [N, F] = fp16(silu(x @ w1.T)) * (x @ w3.T) on row-interleaved W13."""
+    _need(W13, torch.int8, "W13"); _need(w13_scale, torch.float16, "w13_scale")
+    _need(x, torch.float16, "x"); _need(gamma, torch.float16, "gamma")
+    _need(resid, torch.float16, "resid"); _need(h_out, torch.float16, "h_out")
+    M, K = W13.shape
+    F = M // 2
+    N = x.shape[0]
+    Y = out if out is not None else torch.empty((N, F), dtype=torch.float16, device=x.device)
+    check(lib().fa_w8a8_gemm_swiglu(_ptr(W13), _ptr(w13_scale), group_size, _ptr(act_scale),
+                                    _ptr(smooth_inv), _ptr(x), _ptr(resid), _ptr(h_out),
+                                    _ptr(gamma), eps, _ptr(Y), F, N, K, _stream()))
+    return Y
+
+
+def interleave_rows(a, b):
+    """Rows of a and b interleaved: row 2i = a[i], row 2i + 1 = b[i]."""
+    return torch.stack((a, b), dim=1).reshape(2 * a.shape[0], *a.shape[1:]).contiguous()
+
+
+def w8a8_gemm_silu_mul(W, w_scale, gate, up, group_size, act_scale=None, smooth_inv=None,
+                       out=None):
+    """SiLU(gate) * up + linear."""
+    _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale")
+    _need(gate, torch.float16, "gate"); _need(up, torch.float16, "up")
+    M, K = W.shape
+    N = gate.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=gate.device)
+    check(lib().fa_w8a8_gemm_silu_mul(_ptr(W), _ptr(w_scale), group_size, _ptr(act_scale),
+                                      _ptr(smooth_inv), _ptr(gate), _ptr(up), _ptr(Y), M, N, K,
+                                      _stream()))
+    return Y
+
+
 def w8a8_gemm_quantized(W, w_scale, group_size, X_q, X_scale, out=None):
     _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale")
     _need(X_q, torch.int8, "X_q"); _need(X_scale, torch.float32, "X_scale")

@@ -53,6 +53,49 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
                  const uint16_t* act_scale, const uint16_t* smooth_inv,
                  const uint16_t* X, uint16_t* Y, int M, int N, int K, void* stream);
 
+/* Fused prologue + linear for the decode step's attention_norm / ffn_norm
+ * projections (src/engine/dual_ar_engine.cc:576-648: residual_add, rms_norm,
+ * then int8_dequant_gemm_fp16 on the normalised row).  h = x when resid is
+ * NULL, else h = fp16(x + resid) (residual_add, ffn_activations.cu:41-45),
+ * written to h_out [N, K] (required with resid, optional without; must not
+ * overlap x or resid); then rms_norm(h, gamma, eps) (rms_norm.cu:10-58) feeds
+ * fa_w8a8_gemm's quantizer and linear.  Results equal those separate calls
+ * bit for bit.  At N == 1 it is one launch: every workgroup of the GEMV forms
+ * the normalised, quantized token itself.  No reference counterpart as one
+ * call; additive. */
+int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
+                     const uint16_t* act_scale, const uint16_t* smooth_inv,
+                     const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                     const uint16_t* gamma, float eps, uint16_t* Y, int M, int N, int K,
+                     void* stream);
+
+/* The FFN's gate and up projections with the SwiGLU product in their
+ * epilogue: W13 int8 [2F, K] holds w1 and w3 with rows interleaved (row 2i =
+ * w1 row i, row 2i+1 = w3 row i; scales [2F, G] likewise), and act fp16 [N, F]
+ * gets fp16(fp16(silu(gate_i)) * up_i) with gate_i, up_i the fp16 outputs of
+ * the two linears (dual_ar_engine.cc:640-646: two int8_dequant_gemm_fp16,
+ * silu_forward, mul_forward).  gamma non-NULL puts fa_w8a8_gemm_rms's prologue
+ * (residual add into h_out, RMSNorm) in front; gamma NULL quantizes x as
+ * fa_w8a8_gemm does (resid and h_out must then be NULL).  At N == 1 it is one
+ * launch.  Uses that exact input quantization for both halves, so it matches
+ * the reference whenever w1 and w3 share it (no per-weight smooth_inv).  No
+ * reference counterpart as one call; additive. */
+int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_size,
+                        const uint16_t* act_scale, const uint16_t* smooth_inv,
+                        const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                        const uint16_t* gamma, float eps, uint16_t* act, int F, int N, int K,
+                        void* stream);
+
+/* Fused prologue + linear for the FFN down projection: the quantizer sees
+ * fp16(fp16(silu(gate)) * up) (silu_forward then mul_forward,
+ * ffn_activations.cu:12-17, 35-39), then fa_w8a8_gemm's quantizer and linear.
+ * gate, up: fp16 [N, K].  One launch at N == 1.  No reference counterpart as
+ * one call; additive. */
+int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_size,
+                          const uint16_t* act_scale, const uint16_t* smooth_inv,
+                          const uint16_t* gate, const uint16_t* up, uint16_t* Y, int M, int N,
+                          int K, void* stream);
+
 /* The same linear layer on activations that are already quantized (X_q int8
  * [N, K] row-major, X_scale fp32 [N, G]): the part of int8_gemm.cu:423-505
  * after its quantizer launch (:415-421).  Used after the fused prologues

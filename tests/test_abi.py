@@ -58,6 +58,21 @@ def test_invalid_arguments_rejected_without_device():
     assert l.fa_w8a8_gemm_quantized(dummy, dummy, 64, dummy, dummy, dummy, 8, -2, 64, None) == 1
     # empty batch is a no-op (nothing is launched)
     assert l.fa_w8a8_gemm(dummy, dummy, 64, None, None, dummy, dummy, 8, 0, 64, None) == 0
+    # fused prologue entry points: a residual needs h_out, h_out must not alias
+    x, r, h = ctypes.c_void_p(4096), ctypes.c_void_p(1 << 20), ctypes.c_void_p(4096 + 64)
+    rc = l.fa_w8a8_gemm_rms(dummy, dummy, 64, None, None, x, r, None, dummy, 1e-6, dummy,
+                            8, 1, 64, None)
+    assert rc == _lib.FA_ERR_INVALID_ARG and "needs h_out" in l.fa_last_error().decode()
+    rc = l.fa_w8a8_gemm_rms(dummy, dummy, 64, None, None, x, r, h, dummy, 1e-6, dummy,
+                            8, 1, 64, None)
+    assert rc == _lib.FA_ERR_INVALID_ARG and "overlaps" in l.fa_last_error().decode()
+    rc = l.fa_w8a8_gemm_rms(dummy, dummy, 64, None, None, x, None, None, None, 1e-6, dummy,
+                            8, 1, 64, None)
+    assert rc == _lib.FA_ERR_INVALID_ARG   # gamma is required
+    rc = l.fa_w8a8_gemm_silu_mul(dummy, dummy, 64, None, None, dummy, None, dummy, 8, 1, 64, None)
+    assert rc == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_w8a8_gemm_silu_mul(dummy, dummy, 64, None, None, dummy, dummy, dummy, 8, 0, 64,
+                                   None) == 0
     assert l.fa_w8a8_gemm_quantized(dummy, dummy, 64, dummy, dummy, dummy, 0, 4, 64, None) == 0
     # partials window outside the problem
     rc = l.fa_w8a8_gemm_partials(dummy, dummy, 64, dummy, dummy, dummy, dummy, 0, 9, 0, 1,

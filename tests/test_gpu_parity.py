@@ -328,6 +328,88 @@ def test_bin_file_end_to_end():
     assert same(host(Y), ref.w8a8_gemm(q, s, g, x)), "bin"
 
 
+# -------------------------------------------- fused prologue entries ----
+
+@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("name,g", [("qkv", 256), ("gate_up", 64), ("qkv", 128)])
+@pytest.mark.parametrize("with_resid", [True, False])
+def test_gemm_rms_bitexact(name, g, T, with_resid):
+    """fa_w8a8_gemm_rms = residual_add + rms_norm + quant + linear: Y and the
+    residual output h_out bit-identical to the oracle chain (one fused GEMV
+    launch at T == 1, separate launches otherwise)."""
+    K, Nout = LAYER[name]
+    q, s_ = make_linear(Nout, K, g, seed=31)
+    x = synth.activations_f16(T, K, seed=32)
+    gam = synth.gamma_f16(K, seed=33)
+    res = synth.activations_f16(T, K, seed=34) if with_resid else None
+    h_out = torch.empty((T, K), dtype=torch.float16, device="cuda")
+    xd = dev(x)
+    Y = ops.w8a8_gemm_rms(dev(q), dev(s_), xd, dev(gam), 1e-6, g,
+                          resid=dev(res) if with_resid else None, h_out=h_out)
+    h = ref.residual_add(x, res) if with_resid else x
+    rq, rs, _ = ref.rms_norm_quant(h, gam, 1e-6, g)
+    assert same(host(Y), ref.gemm_quantized(q, s_, g, rq, rs))
+    assert same(host(h_out), h)
+    assert same(host(xd), x)   # the input stream is not written
+
+
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("g", [256, 64])
+def test_gemm_silu_mul_bitexact(g, T):
+    K, Nout = LAYER["down"]
+    q, s_ = make_linear(Nout, K, g, seed=41)
+    rng = np.random.default_rng(42)
+    gate = (rng.standard_normal((T, K)) * 2).astype(np.float16)
+    up = rng.standard_normal((T, K)).astype(np.float16)
+    Y = ops.w8a8_gemm_silu_mul(dev(q), dev(s_), dev(gate), dev(up), g)
+    rq, rs, _ = ref.silu_mul_quant(gate, up, g)
+    assert same(host(Y), ref.gemm_quantized(q, s_, g, rq, rs))
+
+
+def test_gemm_rms_small_and_odd_dims():
+    """RMS prologue where the reference reduction has fewer than 1024 threads
+    (dim 384 -> 512 threads, 16 warps; dim 64 -> 64 threads, 2 warps)."""
+    for K, g in ((384, 128), (64, 64)):
+        q, s_ = make_linear(48, K, g, seed=K)
+        x = synth.activations_f16(1, K, seed=K + 1)
+        gam = synth.gamma_f16(K, seed=K + 2)
+        Y = ops.w8a8_gemm_rms(dev(q), dev(s_), dev(x), dev(gam), 1e-6, g)
+        rq, rs, _ = ref.rms_norm_quant(x, gam, 1e-6, g)
+        assert same(host(Y), ref.gemm_quantized(q, s_, g, rq, rs)), K
+
+
+@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("g", [256, 64])
+@pytest.mark.parametrize("mode", ["rms_resid", "rms", "plain"])
+def test_gemm_swiglu_bitexact(g, T, mode):
+    """fa_w8a8_gemm_swiglu on a row-interleaved w1 / w3 weight: act equals
+    the oracle's two linears + silu_mul (fp16 roundings included), h_out the
+    residual add."""
+    K, F = 2560, 1536
+    q1, s1 = make_linear(F, K, g, seed=51)
+    q3, s3 = make_linear(F, K, g, seed=52)
+    q13 = np.stack((q1, q3), axis=1).reshape(2 * F, K)
+    s13 = np.stack((s1, s3), axis=1).reshape(2 * F, -1)
+    x = synth.activations_f16(T, K, seed=53)
+    gam = synth.gamma_f16(K, seed=54)
+    res = synth.activations_f16(T, K, seed=55)
+    h_out = torch.empty((T, K), dtype=torch.float16, device="cuda")
+    if mode == "plain":
+        act = ops.w8a8_gemm_swiglu(dev(q13), dev(s13), dev(x), g)
+        rq, rs = ref.quantize_activations(x, g)
+    else:
+        r = dev(res) if mode == "rms_resid" else None
+        act = ops.w8a8_gemm_swiglu(dev(q13), dev(s13), dev(x), g, gamma=dev(gam), eps=1e-6,
+                                   resid=r, h_out=h_out)
+        h = ref.residual_add(x, res) if mode == "rms_resid" else x
+        rq, rs, _ = ref.rms_norm_quant(h, gam, 1e-6, g)
+        assert same(host(h_out), h)
+    gate = ref.gemm_quantized(q1, s1, g, rq, rs)
+    up = ref.gemm_quantized(q3, s3, g, rq, rs)
+    _, _, ract = ref.silu_mul_quant(gate, up, g)
+    assert same(host(act), ract)
+
+
 # ------------------------------------------------------- decode stack ----
 
 @pytest.mark.parametrize("g,T", [(256, 1), (64, 2)])
@@ -349,8 +431,8 @@ def test_decode_stack_bitexact(g, T):
         xq, xs = ref.quantize_activations(np.ascontiguousarray(y[:, :Q_DIM]), g)
         h = ref.residual_add(h, lin("o", xq, xs))
         xq, xs, _ = ref.rms_norm_quant(h, host(lay["ffn_norm"]), 1e-6, g)
-        y = lin("gate_up", xq, xs)
-        xq, xs, _ = ref.silu_mul_quant(np.ascontiguousarray(y[:, :FFN]),
-                                       np.ascontiguousarray(y[:, FFN:]), g)
+        y = lin("gate_up", xq, xs)      # rows interleaved: gate 2i, up 2i + 1
+        xq, xs, _ = ref.silu_mul_quant(np.ascontiguousarray(y[:, 0::2]),
+                                       np.ascontiguousarray(y[:, 1::2]), g)
         h = ref.residual_add(h, lin("down", xq, xs))
     assert same(host(st.h), h)
