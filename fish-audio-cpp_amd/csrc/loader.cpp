@@ -216,4 +216,66 @@ int fa_bin_quant_meta(const fa_bin* bin, const char* weight_name, fa_quant_meta*
     return FA_OK;
 }
 
+int fa_bin_gate_up(const fa_bin* bin, const char* w1_name, const char* w3_name, int8_t* w13,
+                   uint16_t* s13, fa_quant_meta* meta) {
+    fa::set_last_error("");
+    if (!bin || !w1_name || !w3_name) return FA_ERR_INVALID_ARG;
+    const fish::ModelLoader& L = bin->loader;
+    if (!L.has(w1_name) || !L.has(w3_name)) return FA_ERR_NOT_FOUND;
+    auto fail = [](const std::string& m) {
+        fa::set_last_error("fa_bin_gate_up: " + m);
+        return FA_ERR_INVALID_ARG;
+    };
+    const std::string n1(w1_name), n3(w3_name);
+    const fish::QuantMetaHost m1 = fish::quant_meta_for(L, n1), m3 = fish::quant_meta_for(L, n3);
+    const fish::TensorView v1 = L.get(n1), v3 = L.get(n3);
+    if (v1.dtype != fish::DType::INT8 || v3.dtype != fish::DType::INT8 || !m1.has_scale ||
+        !m3.has_scale)
+        return fail("w1 and w3 must be int8 weights with fp16 scales");
+    if (m1.M != m3.M || m1.K != m3.K || m1.groups != m3.groups || m1.group_size != m3.group_size)
+        return fail("w1 and w3 differ in shape or group size");
+    // one input quantization feeds both halves: their smooth_inv and static
+    // act_scale companions must agree (absent in both, or byte-identical)
+    for (const char* sfx : {"_smooth_inv", "_act_scale"}) {
+        const bool h1 = L.has(n1 + sfx), h3 = L.has(n3 + sfx);
+        if (h1 != h3) return fail(std::string("only one of w1 / w3 has ") + (sfx + 1));
+        if (h1) {
+            const fish::TensorView a = L.get(n1 + sfx), c = L.get(n3 + sfx);
+            const size_t na = (size_t)a.numel() * 2, nc = (size_t)c.numel() * 2;
+            if (na != nc || std::memcmp(a.data, c.data, na) != 0)
+                return fail(std::string("w1 and w3 ") + (sfx + 1) +
+                            " differ: their inputs quantize differently");
+        }
+    }
+    const fish::TensorView sv1 = L.get(n1 + "_scale"), sv3 = L.get(n3 + "_scale");
+    if (sv1.dtype != fish::DType::FP16 || sv3.dtype != fish::DType::FP16 ||
+        sv1.numel() != m1.M * m1.groups || sv3.numel() != sv1.numel())
+        return fail("scale tensors are not fp16 [M] / [M, G]");
+    if (meta) {
+        meta->has_scale = 1;
+        meta->has_smooth_inv = m1.has_smooth_inv;
+        meta->has_act_scale = m1.has_act_scale;
+        meta->group_size = m1.group_size;
+        meta->M = 2 * m1.M;
+        meta->K = m1.K;
+        meta->groups = m1.groups;
+    }
+    const size_t K = (size_t)m1.K, G = (size_t)m1.groups;
+    const int8_t* a = static_cast<const int8_t*>(v1.data);
+    const int8_t* c = static_cast<const int8_t*>(v3.data);
+    const uint16_t* sa = static_cast<const uint16_t*>(sv1.data);
+    const uint16_t* sc = static_cast<const uint16_t*>(sv3.data);
+    for (int64_t i = 0; i < m1.M; ++i) {
+        if (w13) {
+            std::memcpy(w13 + (2 * i) * K, a + i * K, K);
+            std::memcpy(w13 + (2 * i + 1) * K, c + i * K, K);
+        }
+        if (s13) {
+            std::memcpy(s13 + (2 * i) * G, sa + i * G, G * 2);
+            std::memcpy(s13 + (2 * i + 1) * G, sc + i * G, G * 2);
+        }
+    }
+    return FA_OK;
+}
+
 }  // extern "C"

@@ -72,6 +72,7 @@ SIGNATURES = {
     "fa_bin_tensor_at": (_i, [_p, _i, ctypes.POINTER(TensorInfo)]),
     "fa_bin_find": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
     "fa_bin_quant_meta": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(QuantMeta)]),
+    "fa_bin_gate_up": (_i, [_p, ctypes.c_char_p, ctypes.c_char_p, _p, _p, ctypes.POINTER(QuantMeta)]),
     "fa_infer_group_size": (_i, [_i64, _i, _i64]),
 }
 

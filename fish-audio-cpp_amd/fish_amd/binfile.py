@@ -11,7 +11,7 @@ import struct
 
 import numpy as np
 
-from ._lib import FA_OK, FaError, QuantMeta, TensorInfo, lib
+from ._lib import FA_OK, FaError, QuantMeta, TensorInfo, check, lib
 
 MAGIC = 0x46495348
 FORMAT_VERSION = 1
@@ -91,6 +91,20 @@ class BinFile:
             lib().fa_bin_tensor_at(self._h, i, ctypes.byref(ti))
             out.append(ti.name.decode())
         return out
+
+    def gate_up(self, w1, w3):
+        """(W13 int8 [2F, K], S13 fp16 [2F] or [2F, G], QuantMeta): w1 and w3
+        row-interleaved for fa_w8a8_gemm_swiglu."""
+        meta = QuantMeta()
+        rc = lib().fa_bin_gate_up(self._h, w1.encode(), w3.encode(), None, None,
+                                  ctypes.byref(meta))
+        check(rc)
+        F2, K, G = meta.M, meta.K, meta.groups
+        w13 = np.empty((F2, K), np.int8)
+        s13 = np.empty((F2, G) if self.info(w1 + "_scale").ndim > 1 else (F2,), np.float16)
+        check(lib().fa_bin_gate_up(self._h, w1.encode(), w3.encode(), w13.ctypes.data,
+                                   s13.ctypes.data, None))
+        return w13, s13, meta
 
     def array(self, name):
         ti = self.info(name)

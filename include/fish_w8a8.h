@@ -217,6 +217,17 @@ int fa_bin_tensor_at(const fa_bin* bin, int index, fa_tensor_info* info);
 /* ModelLoader::get / has (loader.cc:155-170); FA_ERR_NOT_FOUND if absent. */
 int fa_bin_find(const fa_bin* bin, const char* name, fa_tensor_info* info);
 int fa_bin_quant_meta(const fa_bin* bin, const char* weight_name, fa_quant_meta* meta);
+/* The FFN's w1 and w3 (feed_forward.w1 / .w3, with their _scale companions)
+ * as one row-interleaved int8 weight for fa_w8a8_gemm_swiglu: row 2i = w1 row
+ * i, row 2i+1 = w3 row i, scales likewise ([2F] or [2F, G]), on the host.
+ * Replaces the two separate uploads DualAREngine::init makes
+ * (dual_ar_engine.cc:194-278) when both halves share one input quantization:
+ * FA_ERR_INVALID_ARG when only one has a _smooth_inv / _act_scale or theirs
+ * differ (then the reference's two quantized_gemm calls see different int8
+ * inputs and cannot be fused).  w13 (2F * K bytes) and s13 may be NULL to
+ * only check and fill meta (M = 2F). */
+int fa_bin_gate_up(const fa_bin* bin, const char* w1_name, const char* w3_name, int8_t* w13,
+                   uint16_t* s13, fa_quant_meta* meta);
 /* infer_group_size_from_scale (dual_ar_engine.cc:17-24). */
 int fa_infer_group_size(int64_t K, int scale_ndim, int64_t scale_groups);
 

@@ -98,3 +98,54 @@ def test_bad_files(tmpbin, tmp_path):
             BinFile(tr)
         assert e.value.code == _lib.FA_ERR_FORMAT, cut
         assert _lib.lib().fa_last_error().decode()
+
+
+def _ffn(F=48, K=512, g=64, smooth=(None, None), act=(None, None), seed=1):
+    rng = np.random.default_rng(seed)
+    G = K // g
+    t = []
+    for name, sm, ac in (("w1", smooth[0], act[0]), ("w3", smooth[1], act[1])):
+        w = "layers.0.feed_forward.%s.weight" % name
+        t.append((w, rng.integers(-127, 128, (F, K), dtype=np.int8)))
+        t.append((w + "_scale", (rng.random((F, G)) * 1e-3 + 1e-4).astype(np.float16)))
+        if sm is not None:
+            t.append((w + "_smooth_inv", np.full(K, sm, np.float16)))
+        if ac is not None:
+            t.append((w + "_act_scale", np.full(G, ac, np.float16)))
+    return t
+
+
+W1, W3 = "layers.0.feed_forward.w1.weight", "layers.0.feed_forward.w3.weight"
+
+
+def test_gate_up_interleave(tmpbin):
+    """w1 / w3 -> one row-interleaved weight (row 2i = w1[i], 2i+1 = w3[i])."""
+    tensors = _ffn(smooth=(0.5, 0.5), act=(0.04, 0.04))
+    write_bin(tmpbin, tensors)
+    d = dict(tensors)
+    with BinFile(tmpbin) as b:
+        w13, s13, meta = b.gate_up(W1, W3)
+    assert meta.M == 96 and meta.K == 512 and meta.groups == 8 and meta.group_size == 64
+    assert (meta.has_smooth_inv, meta.has_act_scale) == (1, 1)
+    assert np.array_equal(w13[0::2], d[W1]) and np.array_equal(w13[1::2], d[W3])
+    assert np.array_equal(s13[0::2], d[W1 + "_scale"]) and np.array_equal(s13[1::2], d[W3 + "_scale"])
+
+
+@pytest.mark.parametrize("smooth,act", [((0.5, None), (None, None)),   # only one calibrated
+                                        ((0.5, 0.25), (None, None)),   # different smooth_inv
+                                        ((None, None), (0.04, 0.05))])  # different static scales
+def test_gate_up_rejects_different_input_quantization(tmpbin, smooth, act):
+    write_bin(tmpbin, _ffn(smooth=smooth, act=act))
+    with BinFile(tmpbin) as b:
+        with pytest.raises(_lib.FaError, match="fa_bin_gate_up"):
+            b.gate_up(W1, W3)
+
+
+def test_gate_up_shape_mismatch(tmpbin):
+    t = _ffn()
+    t[2] = (W3, np.zeros((40, 512), np.int8))
+    t[3] = (W3 + "_scale", np.ones((40, 8), np.float16))
+    write_bin(tmpbin, t)
+    with BinFile(tmpbin) as b:
+        with pytest.raises(_lib.FaError, match="differ in shape"):
+            b.gate_up(W1, W3)

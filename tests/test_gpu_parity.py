@@ -328,6 +328,29 @@ def test_bin_file_end_to_end():
     assert same(host(Y), ref.w8a8_gemm(q, s, g, x)), "bin"
 
 
+def test_bin_gate_up_swiglu_end_to_end():
+    """feed_forward.w1 / .w3 written separately in the dual_ar.bin layout,
+    interleaved by the loader (fa_bin_gate_up), run through the SwiGLU GEMV:
+    the activation equals the oracle's two linears + silu_mul."""
+    K, F, g = 2560, 1024, 256
+    q1, s1 = make_linear(F, K, g, seed=61)
+    q3, s3 = make_linear(F, K, g, seed=62)
+    w1 = "text_model.model.layers.0.feed_forward.w1.weight"
+    w3 = "text_model.model.layers.0.feed_forward.w3.weight"
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "dual_ar.bin")
+        write_bin(path, [(w1, q1), (w1 + "_scale", s1), (w3, q3), (w3 + "_scale", s3)])
+        with BinFile(path) as b:
+            w13, s13, meta = b.gate_up(w1, w3)
+    x = synth.activations_f16(1, K, seed=63)
+    gam = synth.gamma_f16(K, seed=64)
+    act = ops.w8a8_gemm_swiglu(dev(w13), dev(s13), dev(x), meta.group_size, gamma=dev(gam))
+    rq, rs, _ = ref.rms_norm_quant(x, gam, 1e-6, g)
+    _, _, ract = ref.silu_mul_quant(ref.gemm_quantized(q1, s1, g, rq, rs),
+                                    ref.gemm_quantized(q3, s3, g, rq, rs), g)
+    assert same(host(act), ract)
+
+
 # -------------------------------------------- fused prologue entries ----
 
 @pytest.mark.parametrize("T", [1, 3])
