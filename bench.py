@@ -234,6 +234,19 @@ def run_secondary(torch, ops, st, args):
     del st
     torch.cuda.empty_cache()
 
+    # the fp16 tied-embedding logits head (155776 x 2560, 0.8 GB), one token;
+    # two weight copies alternate so each launch reads from HBM
+    Wl = [(torch.randn(155776, 2560, device="cuda") * 0.02).half() for _ in range(2)]
+    xl = torch.randn(1, 2560, device="cuda").half()
+    yl = torch.empty(1, 155776, device="cuda", dtype=torch.float16)
+    us = graph_us_per_call(torch, [(lambda W=W: ops.gemm_fp16(W, xl, out=yl)) for W in Wl] * 4,
+                           reps=5)
+    lb = 155776 * 2560 * 2 + 2 * (2560 + 155776)
+    out["logits_fp16_m1_us"] = round(us, 2)
+    out["logits_fp16_m1_GBs"] = round(lb / (us * 1e-6) / 1e9, 1)
+    del Wl
+    torch.cuda.empty_cache()
+
     # M=8, g64 (smaller layer count keeps the bench short)
     st8 = DecodeStack(n_layers=12, g=64, tokens=8, seed=1)
     for name, (K, N) in LAYER_SHAPES.items():

@@ -366,6 +366,24 @@ int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_si
                             s);
 }
 
+int fa_gemm_fp16(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                 void* stream) {
+    const char* fn = "fa_gemm_fp16";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !X || !Y) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    hipStream_t s = (hipStream_t)stream;
+    if (aligned16(W) && aligned16(X) && fa::gemv_f16_ok(M, N, K) && N <= 64) {
+        FA_HIP(fa::launch_gemv_f16(W, X, Y, M, N, K, s));
+        return FA_OK;
+    }
+    if (N > 65535) return fail(FA_ERR_INVALID_ARG, "%s: N=%d too large", fn, N);
+    FA_HIP(fa::launch_gemm_f16_generic(W, X, Y, M, N, K, s));
+    return FA_OK;
+}
+
 int fa_quantize_activations(const uint16_t* X, const uint16_t* act_scale,
                             const uint16_t* smooth_inv, int8_t* X_q, float* X_scale, int N, int K,
                             int group_size, void* stream) {

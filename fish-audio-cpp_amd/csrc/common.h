@@ -191,6 +191,16 @@ hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
                             int K, int g, int G, hipStream_t stream, int variant = 0);
 
+// fp16 x fp16 -> fp16 linear with fp32 accumulation (the FP16 weight path):
+// a streaming GEMV for K % 8 == 0, K <= 4096 and 16-byte aligned W / X
+// (tokens in chunks of up to 8, each chunk reads W once), and an any-shape
+// kernel (N <= 65535).
+bool gemv_f16_ok(int M, int N, int K);
+hipError_t launch_gemv_f16(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                           hipStream_t stream);
+hipError_t launch_gemm_f16_generic(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N,
+                                   int K, hipStream_t stream);
+
 // Any-shape fallback (any K, any group size, unaligned pointers).
 hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                                const float* x_scale, uint16_t* Y, int32_t* dbg_partials,

@@ -52,6 +52,7 @@ SIGNATURES = {
     "fa_w8a8_gemm": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_rms": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _f, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_silu_mul": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_gemm_fp16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_swiglu": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _f, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_quantized": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_partials": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p]),

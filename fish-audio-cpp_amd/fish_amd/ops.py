@@ -61,6 +61,16 @@ def w8a8_gemm_rms(W, w_scale, x, gamma, eps, group_size, resid=None, h_out=None,
     return Y
 
 
+def gemm_fp16(W, X, out=None):
+    """gemm_fp16: Y[n, m] = fp16(sum_k W[m, k] X[n, k]) with fp32 accumulation."""
+    _need(W, torch.float16, "W"); _need(X, torch.float16, "X")
+    M, K = W.shape
+    N = X.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=X.device)
+    check(lib().fa_gemm_fp16(_ptr(W), _ptr(X), _ptr(Y), M, N, K, _stream()))
+    return Y
+
+
 def w8a8_gemm_swiglu(W13, w13_scale, x, group_size, gamma=None, eps=1e-6, resid=None,
                      h_out=None, act_scale=None, smooth_inv=None, out=None):
     """act [N, F] = fp16(silu(x @ w1.T)) * (x @ w3.T) on row-interleaved W13."""

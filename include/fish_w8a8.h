@@ -53,6 +53,16 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
                  const uint16_t* act_scale, const uint16_t* smooth_inv,
                  const uint16_t* X, uint16_t* Y, int M, int N, int K, void* stream);
 
+/* The FP16 weight path of DualAREngine::quantized_gemm
+ * (dual_ar_engine.cc:338-341): gemm_fp16 (dac_engine.cc:19-32), i.e.
+ * cublasGemmEx with fp16 W [M, K], fp16 X [N, K], fp16 Y (col-major [M, N],
+ * ld = M) and CUBLAS_COMPUTE_32F; used for the tied-embedding logits head
+ * (get_logits, dual_ar_engine.cc:663-665).  fp32 accumulation in an order of
+ * its own (cuBLAS's is unspecified), fp16 round-to-nearest output.  The
+ * cublasHandle_t argument has no counterpart. */
+int fa_gemm_fp16(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                 void* stream);
+
 /* Fused prologue + linear for the decode step's attention_norm / ffn_norm
  * projections (src/engine/dual_ar_engine.cc:576-648: residual_add, rms_norm,
  * then int8_dequant_gemm_fp16 on the normalised row).  h = x when resid is

@@ -36,6 +36,7 @@ _SIGS = {
     "orc_mul": (None, [_p, _p, _i64]),
     "orc_residual_add": (None, [_p, _p, _i64]),
     "orc_silu_mul_quant": (None, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i]),
+    "orc_gemm_fp16_exact": (None, [_p, _p, _p, _p, _i, _i, _i]),
     "orc_num_threads": (_i, []),
     "orc_set_num_threads": (None, [_i]),
 }
@@ -206,6 +207,29 @@ def silu_mul_quant(gate, up, group_size, smooth_inv=None, act_scale=None):
     lib().orc_silu_mul_quant(_ptr(gate), _ptr(up), _ptr(smooth_inv), _ptr(act_scale), group_size,
                              _ptr(xq), _ptr(xs), _ptr(out), n, d)
     return xq, xs, out
+
+
+def gemm_fp16_exact(W, X):
+    """(Y, sum |w x|) in float64, both [N, M], for fp16 W [M, K], X [N, K]."""
+    W = _c(W, np.float16)
+    X = _c(X, np.float16)
+    M, K = W.shape
+    N = X.shape[0]
+    Y = np.empty((N, M), np.float64)
+    A = np.empty((N, M), np.float64)
+    lib().orc_gemm_fp16_exact(_ptr(W), _ptr(X), _ptr(Y), _ptr(A), M, N, K)
+    return Y, A
+
+
+def fp16_linear_tolerance(y_exact, abs_sum):
+    """Allowed |y - y_exact| for an fp16 output of an fp32-accumulated sum:
+    one fp16 ulp of the exact value (or 1e-3 relative), plus 2^-18 * sum |w x|
+    for the fp32 accumulation: a lane chain of at most 4 * K / 512 + 4 fp32
+    additions plus a 6-level tree, each rounding at most 2^-24 of a partial
+    bounded by sum |w x| (fp16 products are exact in fp32)."""
+    y16 = np.abs(y_exact).astype(np.float16)
+    ulp = np.spacing(y16).astype(np.float64)
+    return np.maximum(ulp, 1e-3 * np.abs(y_exact)) + abs_sum * 2.0 ** -18
 
 
 def rms_inv(sum_sq, dim, eps):

@@ -28,6 +28,8 @@
  *                                (tests/test_kernels.cu:121-247) plus float64.
  *   orc_silu / orc_mul / orc_residual_add  the reference's closed-form tests
  *                                (tests/test_kernels.cu:354-481) plus float64.
+ *   orc_gemm_fp16_exact          exact rational sums (Python fractions) on
+ *                                small inputs and one-hot closed forms.
  * The reference's CUDA intrinsics rsqrtf/expf are approximations whose
  * constants are not reproduced: this oracle uses (float)(1/sqrt(double)) and
  * (float)exp(double) instead, and the device code uses the same formulas.
@@ -402,4 +404,29 @@ void orc_set_num_threads(int n) {
 #else
     (void)n;
 #endif
+}
+
+/* ------------------------------------------------------- fp16 linear ---- */
+
+void orc_gemm_fp16_exact(const uint16_t* W, const uint16_t* X, double* Y, double* absY,
+                         int M, int N, int K) {
+    /* gemm_fp16 (dac_engine.cc:19-32): cublasGemmEx, fp16 W [M, K] and X
+     * [N, K], CUBLAS_COMPUTE_32F, fp16 Y.  cuBLAS's summation order is not
+     * specified, so this oracle gives the value it approximates: the sum in
+     * double (every fp16 product is exact in double; K <= 2^20 terms keep the
+     * double sum within 2^-32 relative of the exact one), plus sum |w x| for
+     * the caller's fp32-accumulation tolerance.  Y and absY are [N, M]. */
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)N * M; ++i) {
+        const int n = (int)(i / M), m = (int)(i % M);
+        double s = 0.0, a = 0.0;
+        for (int k = 0; k < K; ++k) {
+            const double p = (double)orc_h2f(W[(int64_t)m * K + k]) *
+                             (double)orc_h2f(X[(int64_t)n * K + k]);
+            s += p;
+            a += fabs(p);
+        }
+        Y[i] = s;
+        absY[i] = a;
+    }
 }

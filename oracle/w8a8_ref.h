@@ -99,6 +99,10 @@ void orc_silu_mul_quant(const uint16_t* gate, const uint16_t* up,
 int orc_num_threads(void);
 void orc_set_num_threads(int n);
 
+/* fp16 linear as an exact value: Y, sum|w x| [N, M] in double. */
+void orc_gemm_fp16_exact(const uint16_t* W, const uint16_t* X, double* Y, double* absY,
+                         int M, int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -351,6 +351,42 @@ def test_bin_gate_up_swiglu_end_to_end():
     assert same(host(act), ract)
 
 
+# ------------------------------------------------------- fp16 linear ----
+
+def check_fp16_linear(W, X, Y, rows=None):
+    """|Y - exact| within ref.fp16_linear_tolerance (1 fp16 ulp or 1e-3 rel.,
+    plus 2^-18 * sum |w x| for fp32 accumulation in any order)."""
+    Wh, Xh, Yh = host(W), host(X), host(Y)
+    if rows is not None:
+        Wh, Yh = Wh[rows], Yh[:, rows]
+    ye, ab = ref.gemm_fp16_exact(Wh, Xh)
+    err = np.abs(Yh.astype(np.float64) - ye)
+    assert np.all(err <= ref.fp16_linear_tolerance(ye, ab)), float(err.max())
+
+
+@pytest.mark.parametrize("N,M,K", [(1, 1000, 2560), (3, 777, 2560), (8, 512, 4096), (11, 300, 512),
+                                   (2, 64, 100), (1, 40, 8192)])
+def test_gemm_fp16(N, M, K):
+    """fa_gemm_fp16 (gemm_fp16's cublasGemmEx fp16 / COMPUTE_32F semantics):
+    streaming GEMV (K % 8 == 0, K <= 4096; token chunks 8/4/2/1) and the
+    any-shape kernel (K = 100, K = 8192)."""
+    torch.manual_seed(N * M + K)
+    W = (torch.randn(M, K, device="cuda") * 0.05).half()
+    X = torch.randn(N, K, device="cuda").half()
+    check_fp16_linear(W, X, ops.gemm_fp16(W, X))
+
+
+def test_gemm_fp16_logits_head():
+    """The tied-embedding logits head at full size (155776 x 2560, 0.8 GB of
+    fp16 weight, one token), checked on every 97th row and the last."""
+    torch.manual_seed(9)
+    W = (torch.randn(155776, 2560, device="cuda") * 0.02).half()
+    X = torch.randn(1, 2560, device="cuda").half()
+    Y = ops.gemm_fp16(W, X)
+    rows = np.unique(np.concatenate([np.arange(0, 155776, 97), [155775]]))
+    check_fp16_linear(W, X, Y, rows=rows)
+
+
 # -------------------------------------------- fused prologue entries ----
 
 @pytest.mark.parametrize("T", [1, 3])

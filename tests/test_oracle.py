@@ -298,3 +298,29 @@ def test_group_helpers():
     assert l.orc_infer_group_size(2560, 2, 1) == 2560
     assert l.orc_infer_group_size(2560, 2, 10) == 256
     assert l.orc_infer_group_size(100, 2, 3) == 34
+
+
+# ----------------------------------------------------------- fp16 linear ----
+
+def test_gemm_fp16_exact_rational():
+    """The double-precision fp16 linear equals the exact rational sum (Python
+    fractions over the fp16 values) on small random inputs, and one-hot rows
+    select single products exactly."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    W = (rng.standard_normal((5, 37)) * 0.3).astype(np.float16)
+    X = (rng.standard_normal((3, 37)) * 2).astype(np.float16)
+    Y, A = ref.gemm_fp16_exact(W, X)
+    for n in range(3):
+        for m in range(5):
+            s = sum(Fraction(float(W[m, k])) * Fraction(float(X[n, k])) for k in range(37))
+            a = sum(abs(Fraction(float(W[m, k])) * Fraction(float(X[n, k]))) for k in range(37))
+            assert Y[n, m] == float(s) and A[n, m] == float(a)
+    # one-hot weight rows: row m picks X[:, m] (times 1) exactly
+    W1 = np.zeros((4, 8), np.float16)
+    for m in range(4):
+        W1[m, 2 * m] = 1.0
+    Y1, _ = ref.gemm_fp16_exact(W1, X[:, :8])
+    assert np.array_equal(Y1, X[:, [0, 2, 4, 6]].astype(np.float64))
+    # a transposed operand or a swapped output index fails
+    assert not np.allclose(ref.gemm_fp16_exact(W, X)[0], ref.gemm_fp16_exact(W, X)[0][:, ::-1])
