@@ -185,11 +185,14 @@ hipError_t launch_gemm_pipe(const int8_t* W, const uint16_t* w_scale, const int8
 // (gemm_pipe_tables_bytes) and the same two launches as launch_gemm_pipe.
 bool gemm_tile_ok(int M, int N, int K, int g);
 // variant: 0 = by shape (gemm_tile_choice), 1 = 256 x 128 tiles, 2 = 128 x 128.
+// scales: -1 = by group size, 0 = group-major tables (extra launch), 1 = gathered
+// in-kernel from the given layouts.
 int gemm_tile_choice(int M, int N, int K, int g);
 hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                             const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
-                            int K, int g, int G, hipStream_t stream, int variant = 0);
+                            int K, int g, int G, hipStream_t stream, int variant = 0,
+                            int scales = -1);
 
 // fp16 x fp16 -> fp16 linear with fp32 accumulation (the FP16 weight path):
 // a streaming GEMV for K % 8 == 0, K <= 4096 and 16-byte aligned W / X

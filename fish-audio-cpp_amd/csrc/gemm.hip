@@ -565,12 +565,19 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 // of one block overlaps the matrix work of the others.
 // kAb (measurement builds only; 0 in the library): 1 drops the MFMAs, 2 the
 // fragment reads, 4 the epilogue, 8 the global->LDS loads.
-template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, int kAb = 0, bool kSched = true>
+//
+// DIRECT: the scales come straight from the reference layouts instead of the
+// group-major tables: weight lane r fetches the aligned fp16 pair that holds
+// w_scale[row, g] (4 bytes; the epilogue picks the half), token lanes fetch
+// x_scale[tok, g].  One gather instruction per wave and group, cheap while a
+// row's G scales are few (g >= 128 here), and no table launch.
+template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, int kAb = 0, bool kSched = true,
+          bool DIRECT = false>
 __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ wsT,
     const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G, int tiles_m,
-    int tiles_n) {
+    int tiles_n, const uint16_t* __restrict__ w_scale, const float* __restrict__ x_scale) {
     constexpr int NW = BM * BN / 4096;
     constexpr int WMN = BM / 64;             // waves along the weight rows
     constexpr int AJ = BN * 8 / 64 / NW;     // token-tile loads per wave and stage
@@ -628,6 +635,22 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     const float* const ssrc = tid < BM ? wsT + min(m0 + tid, M - 1)
                                        : xsT + min(n0 + (stk < 0 ? stk + BN : stk), N - 1);
     const size_t sstride = tid < BM ? (size_t)M : (size_t)N;
+    // DIRECT: element index of this lane's scale row in w_scale (row * G) or
+    // x_scale (tok * G); the fp16 pair fetched is clamped inside [0, M * G)
+    const int64_t MG = (int64_t)M * G;
+    const int64_t srow = tid < BM ? (int64_t)min(m0 + tid, M - 1) * G
+                                  : (int64_t)min(n0 + (stk < 0 ? stk + BN : stk), N - 1) * G;
+    auto scale_src = [&](int gn) -> const void* {
+        if constexpr (DIRECT) {
+            if (tid < BM) {
+                const int64_t lo = min((srow + gn) & ~(int64_t)1, MG - 2);
+                return w_scale + lo;
+            }
+            return x_scale + srow + gn;
+        } else {
+            return ssrc + (size_t)gn * sstride;
+        }
+    };
 
     const int nsub = K >> 6;                 // 64-byte substeps
     const int nst = nsub >> 1;               // 128-byte stages
@@ -649,7 +672,7 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int gn = (2 * sc_st + q) >> LGS;
-            dma4(ssrc + (size_t)gn * sstride, lds_addr(&sc[gn & (NSS - 1)][sslot * 64]));
+            dma4(scale_src(gn), lds_addr(&sc[gn & (NSS - 1)][sslot * 64]));
         }
     };
 
@@ -700,7 +723,15 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
         const float* s = sc[gi & (NSS - 1)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            sv.ws[j] = s[brow0 + j * 32];
+            if constexpr (DIRECT) {
+                // the word holds the fp16 pair starting at lo; pick row * G + gi
+                const int64_t idx = (int64_t)min(m0 + brow0 + j * 32, M - 1) * G + gi;
+                const int64_t lo = min(idx & ~(int64_t)1, MG - 2);
+                const uint32_t w2 = __builtin_bit_cast(uint32_t, s[brow0 + j * 32]);
+                sv.ws[j] = h2f((uint16_t)(idx != lo ? w2 >> 16 : w2 & 0xffffu));
+            } else {
+                sv.ws[j] = s[brow0 + j * 32];
+            }
             sv.nws[j] = -(kMagicF * sv.ws[j]);
         }
 #pragma unroll
@@ -1009,32 +1040,45 @@ int gemm_tile_choice(int M, int N, int K, int g) {
 hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                             const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
-                            int K, int g, int G, hipStream_t stream, int variant) {
+                            int K, int g, int G, hipStream_t stream, int variant, int scales) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
     int lg_spg = 0;
     while ((64 << lg_spg) < g) ++lg_spg;
     float* const wsT = tables;
     float* const xsT = tables + (size_t)G * M;
-    int tr = 64;
-    while (tr > 1 && (size_t)tr * G * sizeof(float) > 32768) tr >>= 1;
-    const int wblocks = ceil_div(M, tr);
-    hipLaunchKernelGGL(scale_tables_kernel, dim3((unsigned)(wblocks + ceil_div(N, tr))), dim3(256),
-                       (size_t)tr * G * sizeof(float), stream, w_scale, x_scale, wsT, xsT, M, N, G,
-                       tr, wblocks);
     if (variant == 0) variant = gemm_tile_choice(M, N, K, g);
+    // Scales gathered in-kernel from their own layouts (no table launch) on
+    // 128 x 128 tiles at g >= 128; elsewhere the group-major tables are built
+    // first.  Measured on MI355X: the gather saves the 5 us table launch on
+    // 128 x 128 tiles, but slows the 256 x 128 kernel (256 gathered rows per
+    // group in its stage wait) by 6-20 %, and at g64 a row has 4x the groups.
+    const bool can_direct = (int64_t)M * G >= 2 && ((uintptr_t)w_scale & 3) == 0 &&
+                            ((uintptr_t)x_scale & 3) == 0;
+    const bool direct = can_direct && (scales < 0 ? (variant == 2 && g >= 128) : scales == 1);
+    if (!direct) {
+        int tr = 64;
+        while (tr > 1 && (size_t)tr * G * sizeof(float) > 32768) tr >>= 1;
+        const int wblocks = ceil_div(M, tr);
+        hipLaunchKernelGGL(scale_tables_kernel, dim3((unsigned)(wblocks + ceil_div(N, tr))),
+                           dim3(256), (size_t)tr * G * sizeof(float), stream, w_scale, x_scale, wsT,
+                           xsT, M, N, G, tr, wblocks);
+    }
     const int bm = variant == 1 ? 256 : 128;
     const int tm = ceil_div(M, bm);
     const int tn = ceil_div(N, 128);
     const dim3 grid((unsigned)(tm * tn));
-#define FA_TILE(BMV, NSTV, OCCV, LGS)                                                            \
+#define FA_TILE_D(BMV, NSTV, OCCV, LGS, DIR)                                                     \
     if (dbg_partials)                                                                            \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true>), grid,            \
-                           dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, tm,   \
-                           tn);                                                                  \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true, 0, true, DIR>),    \
+                           grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
+                           tm, tn, w_scale, x_scale);                                            \
     else                                                                                         \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false>), grid,           \
-                           dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, tm,   \
-                           tn);
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false, 0, true, DIR>),   \
+                           grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
+                           tm, tn, w_scale, x_scale);
+#define FA_TILE(BMV, NSTV, OCCV, LGS)                                                            \
+    if (direct) { FA_TILE_D(BMV, NSTV, OCCV, LGS, true) }                                        \
+    else { FA_TILE_D(BMV, NSTV, OCCV, LGS, false) }
 #define FA_TILE_G(BMV, NSTV, OCCV)                                                               \
     if (lg_spg == 0) { FA_TILE(BMV, NSTV, OCCV, 0) }                                             \
     else if (lg_spg == 1) { FA_TILE(BMV, NSTV, OCCV, 1) }                                        \
@@ -1046,6 +1090,7 @@ hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8
     }
 #undef FA_TILE_G
 #undef FA_TILE
+#undef FA_TILE_D
     return hipGetLastError();
 }
 

@@ -269,6 +269,8 @@ def test_config3_prefill_subblock(name, N, g):
     (40, 300, 768, 64),     # tile kernel, g64 (two groups per stage)
     (129, 520, 1280, 128),  # tile kernel, g128
     (33, 64, 384, 128),     # K % 256 == 128: pipelined kernel, odd stage count
+    (70, 259, 768, 256),    # tile kernel, in-kernel scale gather, M * G odd (last pair clamped)
+    (40, 333, 256, 256),    # one group: 1-D scales, M odd
     (3, 40, 100, 48),       # K, g not multiples of 64: generic kernel
     (20, 33, 96, 32),       # generic kernel, N > 16
 ])
