@@ -529,6 +529,12 @@ int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_siz
     rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(max_M, max_tokens, G), s);
     ws->st = (float*)p;
     if (rc) return rc;
+    if (max_tokens > 1) {   // fa_w8a8_gemm_swiglu's [N, 2F] linear output (max_M = 2F)
+        p = ws->yt;
+        rc = grow(&p, &ws->yt_bytes, (size_t)max_tokens * (size_t)max_M * 2, s);
+        ws->yt = (uint16_t*)p;
+        if (rc) return rc;
+    }
     return FA_OK;
 }
 
@@ -541,6 +547,7 @@ int fa_workspace_release(void) {
     if (ws->xq) FA_HIP(hipFree(ws->xq));
     if (ws->xs) FA_HIP(hipFree(ws->xs));
     if (ws->st) FA_HIP(hipFree(ws->st));
+    if (ws->yt) FA_HIP(hipFree(ws->yt));
     *ws = Workspace{};
     return FA_OK;
 }

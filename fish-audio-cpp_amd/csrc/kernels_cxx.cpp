@@ -59,4 +59,34 @@ void int8_gemm_quantized_fp16(const int8_t* W, const __half* scale, int group_si
     check(fa_w8a8_gemm_quantized(W, u16(scale), group_size, X_q, X_scale, u16(Y), M, N, K, stream));
 }
 
+void gemm_fp16(int M_out, int N_out, int K, const __half* W, const __half* X, __half* Y,
+               void* /*blas_handle_unused*/, hipStream_t stream) {
+    check(fa_gemm_fp16(u16(W), u16(X), u16(Y), M_out, N_out, K, stream));
+}
+
+void int8_rms_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                        const __half* act_scale, const __half* smooth_inv, const __half* x,
+                        const __half* resid, __half* h_out, const __half* gamma, float eps,
+                        __half* Y, int M, int N, int K, hipStream_t stream) {
+    check(fa_w8a8_gemm_rms(W, u16(scale), group_size, u16(act_scale), u16(smooth_inv), u16(x),
+                           u16(resid), u16(h_out), u16(gamma), eps, u16(Y), M, N, K, stream));
+}
+
+void int8_swiglu_gemm_fp16(const int8_t* W13, const __half* scale13, int group_size,
+                           const __half* act_scale, const __half* smooth_inv, const __half* x,
+                           const __half* resid, __half* h_out, const __half* gamma, float eps,
+                           __half* act, int F, int N, int K, hipStream_t stream) {
+    check(fa_w8a8_gemm_swiglu(W13, u16(scale13), group_size, u16(act_scale), u16(smooth_inv),
+                              u16(x), u16(resid), u16(h_out), u16(gamma), eps, u16(act), F, N, K,
+                              stream));
+}
+
+void int8_silu_mul_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                             const __half* act_scale, const __half* smooth_inv,
+                             const __half* gate, const __half* up, __half* Y, int M, int N, int K,
+                             hipStream_t stream) {
+    check(fa_w8a8_gemm_silu_mul(W, u16(scale), group_size, u16(act_scale), u16(smooth_inv),
+                                u16(gate), u16(up), u16(Y), M, N, K, stream));
+}
+
 }  // namespace fish::kernels

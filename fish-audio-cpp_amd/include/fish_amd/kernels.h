@@ -38,4 +38,25 @@ void int8_gemm_quantized_fp16(const int8_t* W, const __half* scale, int group_si
                               const int8_t* X_q, const float* X_scale, __half* Y, int M, int N,
                               int K, hipStream_t stream = 0);
 
+// The FP16 weight path of DualAREngine::quantized_gemm: gemm_fp16
+// (dac_engine.cc:19-32, same argument order; Y col-major [M_out, N_out]).
+void gemm_fp16(int M_out, int N_out, int K, const __half* W, const __half* X, __half* Y,
+               void* blas_handle_unused, hipStream_t stream = 0);
+
+// Linear layers with their decode prologue / epilogue fused (fa_w8a8_gemm_rms,
+// fa_w8a8_gemm_swiglu, fa_w8a8_gemm_silu_mul in include/fish_w8a8.h): one
+// launch each at one token.
+void int8_rms_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                        const __half* act_scale, const __half* smooth_inv, const __half* x,
+                        const __half* resid, __half* h_out, const __half* gamma, float eps,
+                        __half* Y, int M, int N, int K, hipStream_t stream = 0);
+void int8_swiglu_gemm_fp16(const int8_t* W13, const __half* scale13, int group_size,
+                           const __half* act_scale, const __half* smooth_inv, const __half* x,
+                           const __half* resid, __half* h_out, const __half* gamma, float eps,
+                           __half* act, int F, int N, int K, hipStream_t stream = 0);
+void int8_silu_mul_gemm_fp16(const int8_t* W, const __half* scale, int group_size,
+                             const __half* act_scale, const __half* smooth_inv,
+                             const __half* gate, const __half* up, __half* Y, int M, int N, int K,
+                             hipStream_t stream = 0);
+
 }  // namespace fish::kernels

@@ -189,6 +189,7 @@ int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, in
  * scratch: calls from one thread on two streams that overlap in time race. */
 int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_size,
                          void* stream);
+/* (max_M counts rows as the linears see them: 2F for fa_w8a8_gemm_swiglu.) */
 /* Release this thread's scratch on the current device (waits for the device). */
 int fa_workspace_release(void);
 

@@ -41,7 +41,10 @@ def test_cpp_mirror_symbols_exported():
     for name in ["fish::kernels::int8_dequant_gemm_fp16", "fish::kernels::rms_norm",
                  "fish::kernels::silu_forward", "fish::kernels::mul_forward",
                  "fish::kernels::residual_add", "fish::ModelLoader::load",
-                 "fish::ModelLoader::get", "fish::infer_group_size_from_scale"]:
+                 "fish::ModelLoader::get", "fish::infer_group_size_from_scale",
+                 "fish::kernels::gemm_fp16", "fish::kernels::int8_rms_gemm_fp16",
+                 "fish::kernels::int8_swiglu_gemm_fp16",
+                 "fish::kernels::int8_silu_mul_gemm_fp16"]:
         assert name in out, name
 
 
