@@ -564,7 +564,9 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 // scaling next to that block's first MFMA of the new group, so the VALU work
 // of one block overlaps the matrix work of the others.
 // kAb (measurement builds only; 0 in the library): 1 drops the MFMAs, 2 the
-// fragment reads, 4 the epilogue, 8 the global->LDS loads.
+// fragment reads, 4 the epilogue (one add per block and group remains, so the
+// MFMA chains stay live), 8 the global->LDS loads (the tiles are filled once
+// instead, so the fragment reads stay live).
 //
 // DIRECT: the scales come straight from the reference layouts instead of the
 // group-major tables: weight lane r fetches the aligned fp16 pair that holds
@@ -593,6 +595,14 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     __shared__ __align__(16) int8_t At[NST][BN * 128];   // tokens, 128 B per row and stage
     __shared__ __align__(16) int8_t Bt[NST][BM * 128];   // weight rows
     __shared__ __align__(16) float sc[NSS][BM + BN];     // [0, BM) weight scales, then tokens
+    if constexpr ((kAb & 8) != 0) {
+        // no tile loads: give the fragment reads defined (varying) contents
+        for (int i = threadIdx.x; i < NST * BN * 32; i += blockDim.x)
+            reinterpret_cast<uint32_t*>(At)[i] = (uint32_t)i * 2654435761u;
+        for (int i = threadIdx.x; i < NST * BM * 32; i += blockDim.x)
+            reinterpret_cast<uint32_t*>(Bt)[i] = (uint32_t)i * 40503u + 7u;
+        __syncthreads();
+    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -743,7 +753,11 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     };
     // scale group gi's finished accumulators of block (i, j) into acc
     auto epi = [&](int gi, const Scales& sv, int i, int j) {
-        if constexpr ((kAb & 4) != 0) return;
+        if constexpr ((kAb & 4) != 0) {
+            // one operation per block: keeps every MFMA chain live
+            acc[i][j][0] += __int_as_float(P[i][j][0]);
+            return;
+        }
         const float ws = sv.ws[j];
         const float nws = sv.nws[j];
 #pragma unroll
