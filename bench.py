@@ -221,6 +221,21 @@ def run_secondary(torch, ops, st, args):
     t = (time.perf_counter() - t0) / reps
     out["cfg4_stack_g256_m1"] = {"step_ms": round(t * 1e3, 4),
                                  "GB/s": round(st.stack_bytes() / t / 1e9, 1)}
+    # the same stack as one device-ordered launch (fa_chain; eager: one
+    # cooperative launch plus a counter reset and the last residual add)
+    st.h.copy_(st.h0)
+    st.build_chain()
+    for _ in range(2):
+        st.run_chain()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st.run_chain()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    out["cfg4_chain_g256_m1"] = {"step_ms": round(t * 1e3, 4),
+                                 "GB/s": round(st.stack_bytes() / t / 1e9, 1),
+                                 "complete": st.chain.status() == 0}
     # configs[1] per-linear GEMV time (graph of one launch per layer, cold weights)
     for name, (K, N) in LAYER_SHAPES.items():
         xq, xs = ops.quantize_activations(st.x_in[name], 256)

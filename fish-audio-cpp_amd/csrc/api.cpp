@@ -12,12 +12,14 @@
 // failing HIP call is reported with file/line and hipGetErrorString, here as
 // a status code plus a per-thread message instead of an exception.
 #include "common.h"
+#include "chain.h"
 #include "../../include/fish_w8a8.h"
 
 #include <cstdarg>
 #include <cstdio>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 namespace {
 
@@ -549,6 +551,185 @@ int fa_workspace_release(void) {
     if (ws->st) FA_HIP(hipFree(ws->st));
     if (ws->yt) FA_HIP(hipFree(ws->yt));
     *ws = Workspace{};
+    return FA_OK;
+}
+
+// ------------------------------------------------------------ chain ----
+
+struct fa_chain {
+    int dev = 0;
+    fa::ch::ChainStepDev* d_steps = nullptr;
+    int* d_sync = nullptr;
+    int* d_flags = nullptr;
+    int epoch = 0;
+    fa::ChainPlan plan{};
+};
+
+static void chain_free(fa_chain* c) {
+    if (!c) return;
+    if (c->d_steps) (void)hipFree(c->d_steps);
+    if (c->d_sync) (void)hipFree(c->d_sync);
+    if (c->d_flags) (void)hipFree(c->d_flags);
+    delete c;
+}
+
+int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_chain** out) {
+    const char* fn = "fa_chain_create";
+    g_err.clear();
+    if (!out) return fail(FA_ERR_INVALID_ARG, "%s: null out", fn);
+    *out = nullptr;
+    if (!steps || n_steps <= 0 || n_steps > fa::kChainMaxSteps)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad steps / n_steps=%d", fn, n_steps);
+    if (group_size != 64 && group_size != 128 && group_size != 256)
+        return fail(FA_ERR_INVALID_ARG, "%s: group_size=%d (64, 128 or 256)", fn, group_size);
+    const int g = group_size;
+    const int lg = g == 64 ? 6 : g == 128 ? 7 : 8;
+    const int rows = fa::chain_rows_per_task();
+    const int kmax = fa::chain_max_k();
+    std::vector<fa::ch::ChainStepDev> h((size_t)n_steps);
+    int64_t total = 0;
+    int kp_max = 16, g_pad = 4, kh = 0;
+    for (int i = 0; i < n_steps; ++i) {
+        const fa_chain_step& c = steps[i];
+        if (!c.w || !c.w_scale || !c.x || !c.y)
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: null pointer", fn, i);
+        if (c.m <= 0 || c.m > (1 << 29) || c.k < 16 || c.k > kmax || c.k % 16 != 0 || g > c.k)
+            return fail(FA_ERR_INVALID_ARG,
+                        "%s: step %d: m=%d k=%d (k a multiple of 16 in [group_size, %d])", fn, i,
+                        c.m, c.k, kmax);
+        if (c.prologue != 0 && c.prologue != 2)
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: prologue %d (0 or 2)", fn, i, c.prologue);
+        if (c.epilogue != 0 && c.epilogue != 1)
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: epilogue %d (0 or 1)", fn, i, c.epilogue);
+        if (c.epilogue == 1 && (c.m & 1))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: SwiGLU epilogue needs even m", fn, i);
+        if (c.prologue == 2 && !c.gamma)
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: prologue 2 needs gamma", fn, i);
+        if (c.prologue == 2 && c.k > fa::chain_max_k_pro())
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: prologue 2 takes k <= %d", fn, i,
+                        fa::chain_max_k_pro());
+        if (c.prologue == 0 && (c.x2 || c.gamma || c.h_out))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: x2 / gamma / h_out need prologue 2", fn,
+                        i);
+        if (!aligned16(c.w) || !aligned16(c.x) || (c.x2 && !aligned16(c.x2)) ||
+            (c.gamma && !aligned16(c.gamma)) || (c.h_out && !aligned16(c.h_out)) ||
+            ((uintptr_t)c.y & 3) || ((uintptr_t)c.w_scale & 1))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: misaligned pointer", fn, i);
+        const size_t k = (size_t)c.k;
+        const size_t ny = c.epilogue == 1 ? (size_t)c.m / 2 : (size_t)c.m;
+        if (overlaps(c.y, ny, c.x, k) || overlaps(c.y, ny, c.x2, k) ||
+            overlaps(c.y, ny, c.gamma, k) || overlaps(c.y, ny, c.h_out, k))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: y overlaps an input or h_out", fn, i);
+        if (c.h_out && (overlaps(c.h_out, k, c.x, k) || overlaps(c.h_out, k, c.x2, k) ||
+                        overlaps(c.h_out, k, c.gamma, k)))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: h_out overlaps an input", fn, i);
+        fa::ch::ChainStepDev& d = h[(size_t)i];
+        d.W = c.w;
+        d.w_scale = c.w_scale;
+        d.X = c.x;
+        d.x2 = c.x2;
+        d.gamma = c.gamma;
+        d.h_out = c.h_out;
+        d.Y = c.y;
+        d.M = c.m;
+        d.K = c.k;
+        d.lg_g = lg;
+        d.G = (c.k + g - 1) / g;
+        d.passes = (c.k + 511) / 512;
+        d.nblocks = (c.m + rows - 1) / rows;
+        d.task0 = (int)total;
+        d.pro = c.prologue;
+        d.epi = c.epilogue;
+        d.eps = c.eps;
+        total += d.nblocks;
+        if (total > (1 << 30)) return fail(FA_ERR_INVALID_ARG, "%s: too many rows", fn);
+        const int kp = (c.k + 15) & ~15;
+        kp_max = kp > kp_max ? kp : kp_max;
+        // scale slots the last (padding) pass reads
+        const int gp = (d.passes + fa::kChainRing - 1) / fa::kChainRing * fa::kChainRing * (512 / g);
+        g_pad = gp > g_pad ? gp : g_pad;
+        if (c.prologue == 2) kh = kp > kh ? kp : kh;
+    }
+    g_pad = (g_pad + 3) & ~3;
+    const size_t lds = fa::chain_lds_bytes(kp_max, g_pad, kh);
+    if (lds > 64 * 1024) return fail(FA_ERR_INVALID_ARG, "%s: steps need %zu B of LDS", fn, lds);
+    fa_chain* c = new fa_chain();
+    if (hipGetDevice(&c->dev) != hipSuccess ||
+        hipMalloc((void**)&c->d_steps, h.size() * sizeof(h[0])) != hipSuccess ||
+        hipMalloc((void**)&c->d_sync, (size_t)(n_steps + 2) * sizeof(int)) != hipSuccess ||
+        hipMemcpy(c->d_steps, h.data(), h.size() * sizeof(h[0]), hipMemcpyHostToDevice) !=
+            hipSuccess ||
+        hipMemset(c->d_sync, 0, (size_t)(n_steps + 2) * sizeof(int)) != hipSuccess ||
+        hipMalloc((void**)&c->d_flags, (size_t)n_steps * 8 * 32 * sizeof(int)) != hipSuccess ||
+        hipMemset(c->d_flags, 0, (size_t)n_steps * 8 * 32 * sizeof(int)) != hipSuccess) {
+        chain_free(c);
+        return fail(FA_ERR_HIP, "%s: device allocation / upload failed", fn);
+    }
+    int coop = 0;
+    const int grid = fa::chain_grid(lg, lds);
+    if (grid <= 0 ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->dev) != hipSuccess ||
+        !coop) {
+        chain_free(c);
+        return fail(FA_ERR_HIP, "%s: occupancy query failed or no cooperative launch", fn);
+    }
+    c->plan.steps = c->d_steps;
+    c->plan.sync = c->d_sync;
+    c->plan.flags = c->d_flags;
+    c->plan.nsteps = n_steps;
+    c->plan.total = (int)total;
+    c->plan.lg = lg;
+    c->plan.grid = grid < total ? grid : (int)total;
+    c->plan.spin_limit = 1 << 21;
+    c->plan.kp_max = kp_max;
+    c->plan.g_pad = g_pad;
+    c->plan.kh = kh;
+    c->plan.lds = lds;
+    *out = c;
+    return FA_OK;
+}
+
+int fa_chain_run(fa_chain* chain, void* stream) {
+    const char* fn = "fa_chain_run";
+    g_err.clear();
+    if (!chain) return fail(FA_ERR_INVALID_ARG, "%s: null chain", fn);
+    int dev = 0;
+    FA_HIP(hipGetDevice(&dev));
+    if (dev != chain->dev)
+        return fail(FA_ERR_INVALID_ARG, "%s: chain lives on device %d, current is %d", fn,
+                    chain->dev, dev);
+    // flags hold the epoch of the launch that set them: a new value per launch
+    chain->epoch = chain->epoch == 0x7fffffff ? 1 : chain->epoch + 1;
+    chain->plan.epoch = chain->epoch;
+    FA_HIP(fa::launch_chain(chain->plan, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_chain_status(fa_chain* chain, void* stream) {
+    const char* fn = "fa_chain_status";
+    g_err.clear();
+    if (!chain) return fail(FA_ERR_INVALID_ARG, "%s: null chain", fn);
+    FA_HIP(hipStreamSynchronize((hipStream_t)stream));
+    int e = 0;
+    FA_HIP(hipMemcpy(&e, chain->d_sync + chain->plan.nsteps, sizeof(int),
+                     hipMemcpyDeviceToHost));
+    if (e != 0) return fail(FA_ERR_HIP, "%s: a step's wait for its predecessor gave up", fn);
+    return FA_OK;
+}
+
+int fa_chain_set_spin_limit(fa_chain* chain, int polls) {
+    g_err.clear();
+    if (!chain || polls < 0)
+        return fail(FA_ERR_INVALID_ARG, "fa_chain_set_spin_limit: bad chain / polls");
+    chain->plan.spin_limit = polls;
+    return FA_OK;
+}
+
+int fa_chain_destroy(fa_chain* chain) {
+    g_err.clear();
+    if (!chain) return FA_OK;
+    (void)hipDeviceSynchronize();
+    chain_free(chain);
     return FA_OK;
 }
 

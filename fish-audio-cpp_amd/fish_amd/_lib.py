@@ -45,6 +45,24 @@ class QuantMeta(ctypes.Structure):
     ]
 
 
+class ChainStep(ctypes.Structure):
+    """fa_chain_step (include/fish_w8a8.h)."""
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("w_scale", ctypes.c_void_p),
+        ("x", ctypes.c_void_p),
+        ("x2", ctypes.c_void_p),
+        ("gamma", ctypes.c_void_p),
+        ("h_out", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("m", ctypes.c_int),
+        ("k", ctypes.c_int),
+        ("prologue", ctypes.c_int),
+        ("epilogue", ctypes.c_int),
+        ("eps", ctypes.c_float),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "fa_last_error": (ctypes.c_char_p, []),
@@ -67,6 +85,11 @@ SIGNATURES = {
     "fa_quantize_weights_groupwise": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),
     "fa_workspace_reserve": (_i, [_i, _i, _i, _i, _p]),
     "fa_workspace_release": (_i, []),
+    "fa_chain_create": (_i, [ctypes.POINTER(ChainStep), _i, _i, ctypes.POINTER(_p)]),
+    "fa_chain_run": (_i, [_p, _p]),
+    "fa_chain_status": (_i, [_p, _p]),
+    "fa_chain_set_spin_limit": (_i, [_p, _i]),
+    "fa_chain_destroy": (_i, [_p]),
     "fa_bin_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "fa_bin_close": (None, [_p]),
     "fa_bin_num_tensors": (_i, [_p]),

@@ -142,6 +142,45 @@ class DecodeStack:
         if cur is not self.h:
             self.h.copy_(cur)
 
+    # -- configs[4] as one device-ordered launch (fa_chain) --
+    def build_chain(self):
+        """The steps of run_stack (T == 1) as a fa_chain: the same kernels'
+        arithmetic and the same buffers, one launch for all 4 * n linears."""
+        assert self.T == 1, "the chain serves one-token decode"
+        steps = []
+        cur, nxt = self.h, self.h_alt
+        for li, lay in enumerate(self.layers):
+            L = lay["qkv"]
+            st = dict(w=L.W, w_scale=L.scale, x=cur, y=self.y["qkv"], gamma=lay["attn_norm"],
+                      prologue=2, eps=1e-6)
+            if li != 0:
+                st.update(x2=self.y["down"], h_out=nxt)
+                cur, nxt = nxt, cur
+            steps.append(st)
+            L = lay["o"]
+            steps.append(dict(w=L.W, w_scale=L.scale, x=self.y["qkv"], k=Q_DIM, y=self.y["o"]))
+            L = lay["gate_up"]
+            steps.append(dict(w=L.W, w_scale=L.scale, x=cur, x2=self.y["o"], h_out=nxt,
+                              gamma=lay["ffn_norm"], y=self.act, prologue=2, epilogue=1, eps=1e-6))
+            cur, nxt = nxt, cur
+            L = lay["down"]
+            steps.append(dict(w=L.W, w_scale=L.scale, x=self.act, y=self.y["down"]))
+        self._chain_out = cur
+        self.chain = ops.Chain(steps, self.g)
+        return self.chain
+
+    def run_chain(self):
+        """run_stack's result through one chain launch (+ the last residual add)."""
+        if getattr(self, "chain", None) is None:
+            self.build_chain()
+        self.chain.run()
+        cur = self._chain_out
+        l_ = ops.lib()
+        ops.check(l_.fa_residual_add(cur.data_ptr(), self.y["down"].data_ptr(), HIDDEN,
+                                     ops._stream()))
+        if cur is not self.h:
+            self.h.copy_(cur)
+
     def stack_bytes(self):
         """Algorithmic bytes of one stack pass: int8 W + fp16 scales of all
         linears + gamma + fp16 activations in/out of each linear."""

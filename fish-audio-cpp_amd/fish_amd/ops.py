@@ -5,9 +5,11 @@ in libfish_w8a8.so.  Shapes follow the reference kernel API
 (src/kernels/kernels.h:242-259): W [M, K] int8, w_scale fp16 [M] or [M, G],
 X [N, K] fp16, returned Y is [N, M] fp16 (= the reference's col-major [M, N]).
 """
+import ctypes
+
 import torch
 
-from ._lib import check, lib
+from ._lib import ChainStep, check, lib
 
 
 def _stream():
@@ -218,3 +220,58 @@ def quantize_weights_groupwise(w, group_size):
     check(lib().fa_quantize_weights_groupwise(_ptr(w), rows, K, group_size, _ptr(q), _ptr(s),
                                               _stream()))
     return q, s
+
+
+class Chain:
+    """fa_chain: one-token W8A8 linears run as one device-ordered launch.
+
+    `steps` is a list of dicts of device tensors: w (int8 [m, k]), w_scale
+    (fp16 [m, G]), x (fp16, at least k values), y (fp16 output), and for
+    prologue 2 gamma, optional x2 and h_out; `k` defaults to x.numel(),
+    `prologue` / `epilogue` to 0, `eps` to 1e-6.  The tensors must outlive
+    the chain (it keeps references)."""
+
+    def __init__(self, steps, group_size):
+        arr = (ChainStep * len(steps))()
+        self._keep = []
+        for i, st in enumerate(steps):
+            w, ws, x, y = st["w"], st["w_scale"], st["x"], st["y"]
+            _need(w, torch.int8, "w"); _need(ws, torch.float16, "w_scale")
+            _need(x, torch.float16, "x"); _need(y, torch.float16, "y")
+            for name in ("x2", "gamma", "h_out"):
+                _need(st.get(name), torch.float16, name)
+            c = arr[i]
+            c.w, c.w_scale, c.x, c.y = w.data_ptr(), ws.data_ptr(), x.data_ptr(), y.data_ptr()
+            c.x2, c.gamma, c.h_out = _ptr(st.get("x2")), _ptr(st.get("gamma")), _ptr(st.get("h_out"))
+            c.m = w.shape[0]
+            c.k = st.get("k", x.numel())
+            if w.shape[1] != c.k:
+                raise ValueError("step %d: w is [%d, %d] but k=%d" % (i, w.shape[0], w.shape[1], c.k))
+            c.prologue = st.get("prologue", 0)
+            c.epilogue = st.get("epilogue", 0)
+            c.eps = st.get("eps", 1e-6)
+            self._keep.append(st)
+        h = ctypes.c_void_p()
+        check(lib().fa_chain_create(arr, len(steps), group_size, ctypes.byref(h)))
+        self._h = h
+
+    def run(self):
+        check(lib().fa_chain_run(self._h, _stream()))
+
+    def status(self):
+        """0 when the last run finished; waits for the current stream."""
+        return lib().fa_chain_status(self._h, _stream())
+
+    def set_spin_limit(self, polls):
+        check(lib().fa_chain_set_spin_limit(self._h, polls))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().fa_chain_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

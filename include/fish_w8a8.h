@@ -179,6 +179,59 @@ int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, in
                                   int8_t* q, uint16_t* scale, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Decode chain: a sequence of one-token W8A8 linears as one launch.          */
+/* ------------------------------------------------------------------------ */
+
+/* One linear of a chain.  Step s reads what step s - 1 (and earlier steps)
+ * wrote; the device runs the steps in order, but each step's weight loads
+ * start before the previous step has finished.  Results are bit-identical to
+ * the per-linear entry points:
+ *   prologue 0 = fa_w8a8_gemm at N = 1 (dynamic per-group quantization);
+ *   prologue 2 = fa_w8a8_gemm_rms at N = 1 (h = x + x2 when x2 is given,
+ *                RMSNorm with gamma and eps, quantization; h goes to h_out
+ *                when given);
+ *   epilogue 1 = fa_w8a8_gemm_swiglu's pair epilogue (rows 2i / 2i + 1 are the
+ *                interleaved w1 / w3 rows; y[i] = silu(gate) * up, m / 2
+ *                values).
+ * No act_scale / smooth_inv: the chain serves the dynamic-quantization
+ * decode path.  x, x2, gamma, h_out and w must be 16-byte aligned, y 4-byte
+ * aligned; k a multiple of 16, at least group_size, at most 12288 (4096 with
+ * prologue 2); y and h_out must not overlap the same step's inputs. */
+typedef struct {
+    const int8_t* w;            /* [m, k] int8, row-major                        */
+    const uint16_t* w_scale;    /* [m, ceil(k / group_size)] fp16                */
+    const uint16_t* x;          /* [k] fp16 input (prologue 2: residual stream)  */
+    const uint16_t* x2;         /* prologue 2: residual addend [k], or NULL      */
+    const uint16_t* gamma;      /* prologue 2: RMSNorm weight [k]                */
+    uint16_t* h_out;            /* prologue 2: h = x + x2 written here, or NULL  */
+    uint16_t* y;                /* [m] fp16 (epilogue 0) or [m / 2] (epilogue 1)  */
+    int m, k;
+    int prologue;               /* 0 or 2 (see above)                            */
+    int epilogue;               /* 0 or 1 (see above)                            */
+    float eps;                  /* prologue 2: RMSNorm epsilon                   */
+} fa_chain_step;
+
+typedef struct fa_chain fa_chain;
+
+/* The per-layer launch sequence of DualAREngine::decode_step
+ * (dual_ar_engine.cc:576-648) -- rms_norm + quantize + int8 GEMV per
+ * projection, launch by launch -- as a device-ordered chain.  Validates the
+ * steps and uploads the step table (allocates device memory: call once,
+ * outside a capture).  All steps share group_size (64, 128 or 256). */
+int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_chain** out);
+/* Run the chain on `stream` (a counter reset and one cooperative launch;
+ * no allocation, no host sync).
+ * Runs on one stream at a time: overlapping runs of one chain race. */
+int fa_chain_run(fa_chain* chain, void* stream);
+/* Wait for `stream`, then report whether the last run finished: FA_ERR_HIP
+ * when a step's wait for its predecessor gave up (spin limit reached), in
+ * which case the outputs are incomplete. */
+int fa_chain_status(fa_chain* chain, void* stream);
+/* Upper bound on the polls of one wait (default 1 << 21); testing hook. */
+int fa_chain_set_spin_limit(fa_chain* chain, int polls);
+int fa_chain_destroy(fa_chain* chain);
+
+/* ------------------------------------------------------------------------ */
 /* Scratch.                                                                  */
 /* ------------------------------------------------------------------------ */
 

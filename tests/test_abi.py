@@ -95,6 +95,52 @@ def test_invalid_arguments_rejected_without_device():
     assert l.fa_last_error().decode() == ""
 
 
+def test_chain_rejects_bad_steps_without_device():
+    """fa_chain_create validates every step before any device call (the
+    pointers here are never dereferenced)."""
+    l = _lib.lib()
+    out = ctypes.c_void_p()
+
+    def step(**kw):
+        st = _lib.ChainStep()
+        st.w, st.w_scale, st.x, st.y = 1 << 20, 1 << 21, 1 << 22, 1 << 23
+        st.m, st.k, st.prologue, st.epilogue, st.eps = 64, 256, 0, 0, 1e-6
+        for k, v in kw.items():
+            setattr(st, k, v)
+        return st
+
+    def create(*steps, g=256):
+        arr = (_lib.ChainStep * len(steps))(*steps)
+        return l.fa_chain_create(arr, len(steps), g, ctypes.byref(out))
+
+    bad = [
+        (dict(w=None), "null pointer"),
+        (dict(k=250), "k a multiple of 16"),
+        (dict(k=16384), "k a multiple of 16"),
+        (dict(k=128), "k a multiple of 16"),          # group larger than k
+        (dict(m=0), "m=0"),
+        (dict(prologue=1), "prologue 1"),
+        (dict(epilogue=2), "epilogue 2"),
+        (dict(epilogue=1, m=63), "even m"),
+        (dict(prologue=2), "needs gamma"),
+        (dict(gamma=1 << 24), "need prologue 2"),
+        (dict(x=(1 << 22) + 8), "misaligned"),
+        (dict(y=(1 << 22) + 64), "y overlaps"),
+        (dict(prologue=2, gamma=1 << 24, h_out=(1 << 22) + 16), "h_out overlaps"),
+    ]
+    for kw, msg in bad:
+        assert create(step(**kw)) == _lib.FA_ERR_INVALID_ARG, kw
+        assert msg in l.fa_last_error().decode(), (kw, l.fa_last_error())
+    assert create(step(), g=32) == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_chain_create(None, 1, 256, ctypes.byref(out)) == _lib.FA_ERR_INVALID_ARG
+    arr = (_lib.ChainStep * 1)(step())
+    assert l.fa_chain_create(arr, 0, 256, ctypes.byref(out)) == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_chain_run(None, None) == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_chain_status(None, None) == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_chain_set_spin_limit(None, 5) == _lib.FA_ERR_INVALID_ARG
+    assert l.fa_chain_destroy(None) == 0
+
+
 def test_infer_group_size():
     l = _lib.lib()
     # src/engine/dual_ar_engine.cc:17-24
