@@ -155,10 +155,11 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def graph_us_per_call(torch, calls, reps=10):
-    """Average duration per call of `calls` (a list of closures launching
-    one kernel each on torch's current stream), captured back to back in
-    one HIP graph and timed with events around the replays on that stream."""
+def graph_us_per_call(torch, calls, reps=10, rounds=5):
+    """Duration per call of `calls` (a list of closures launching one kernel
+    each on torch's current stream), captured back to back in one HIP graph:
+    after three warm-up replays, `rounds` rounds of `reps` replays are timed
+    with events on that stream, and the median round is reported."""
     for c in calls:
         c()
     torch.cuda.synchronize()
@@ -166,15 +167,19 @@ def graph_us_per_call(torch, calls, reps=10):
     with torch.cuda.graph(g):
         for c in calls:
             c()
-    g.replay()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
+    for _ in range(3):
         g.replay()
-    e.record()
-    e.synchronize()
-    return s.elapsed_time(e) * 1e3 / (reps * len(calls))
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(rounds):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            g.replay()
+        e.record()
+        e.synchronize()
+        per.append(s.elapsed_time(e) * 1e3 / (reps * len(calls)))
+    return statistics.median(per)
 
 
 def roofline_gate_up(torch, ops, st, LAYER_SHAPES):

@@ -57,7 +57,13 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi)
     if (epi != 0 && (!qx || N != 1 || pro == 1 || (M & 1))) return p;
     if (N == 1 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 16 == 0 && K <= 32768) {
         const int lgroups = g / 16;
-        p.kind = ((M >= 4096 || epi) && lgroups <= 32) ? 2 : 1;   // rows per wave
+        // rows per wave (measured on MI355X over the layer shapes at g256):
+        // one row streams best on staged int8 codes; with in-kernel
+        // quantization (8-wave workgroups, each quantizing the token) two
+        // rows halve the workgroups and win on the large shapes; the SwiGLU
+        // pair needs two
+        const bool two = epi || (qx && (M >= 8192 || K >= 8192));
+        p.kind = (two && lgroups <= 32) ? 2 : 1;
         if (epi && p.kind != 2) return GemvPlan{};
         p.epi = epi;
         const int R = p.kind;
