@@ -80,6 +80,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate_up GEMV event timing (for rocprofv3 runs)")
+    ap.add_argument("--chain-only", action="store_true",
+                    help="only the configs[4] decode chain, 20 runs (for rocprofv3 runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configs[3] M=2048 g256 prefill GEMMs (for rocprofv3 runs)")
     args = ap.parse_args()
@@ -100,6 +102,19 @@ def main():
     log("building 36-layer g256 weight set ...")
     st = DecodeStack(n_layers=args.layers, g=256, tokens=1, seed=0)
     torch.cuda.synchronize()
+
+    if args.chain_only:
+        st.build_chain()
+        t = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            st.run_chain()
+            torch.cuda.synchronize()
+            t.append(time.perf_counter() - t0)
+        print(json.dumps({"chain_step_ms_median": round(statistics.median(t) * 1e3, 4),
+                          "complete": st.chain.status() == 0}), flush=True)
+        st.chain.close()
+        return
 
     if args.roofline_only:
         # The gate_up GEMV, then a plain 64 MiB device copy whose known byte
@@ -241,6 +256,8 @@ def run_secondary(torch, ops, st, args):
     out["cfg4_chain_g256_m1"] = {"step_ms": round(t * 1e3, 4),
                                  "GB/s": round(st.stack_bytes() / t / 1e9, 1),
                                  "complete": st.chain.status() == 0}
+    st.chain.close()
+    st.chain = None
     # configs[1] per-linear GEMV time (graph of one launch per layer, cold weights)
     for name, (K, N) in LAYER_SHAPES.items():
         xq, xs = ops.quantize_activations(st.x_in[name], 256)

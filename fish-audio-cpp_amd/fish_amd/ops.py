@@ -6,6 +6,7 @@ in libfish_w8a8.so.  Shapes follow the reference kernel API
 X [N, K] fp16, returned Y is [N, M] fp16 (= the reference's col-major [M, N]).
 """
 import ctypes
+import sys
 
 import torch
 
@@ -271,6 +272,10 @@ class Chain:
             self._h = None
 
     def __del__(self):
+        # at interpreter exit the HIP runtime may already be gone: leave the
+        # device memory to the process teardown
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
