@@ -80,6 +80,9 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate_up GEMV event timing (for rocprofv3 runs)")
+    ap.add_argument("--stack-only", action="store_true",
+                    help="only the configs[4] four-launch stack, graph-replayed 13 times "
+                         "(for rocprofv3 runs)")
     ap.add_argument("--chain-only", action="store_true",
                     help="only the configs[4] decode chain, 20 runs (for rocprofv3 runs)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -102,6 +105,18 @@ def main():
     log("building 36-layer g256 weight set ...")
     st = DecodeStack(n_layers=args.layers, g=256, tokens=1, seed=0)
     torch.cuda.synchronize()
+
+    if args.stack_only:
+        st.h.copy_(st.h0)
+        g_stack = st.capture(lambda: st.run_stack())
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(13):
+            g_stack.replay()
+        torch.cuda.synchronize()
+        print(json.dumps({"stack_step_ms_mean": round((time.perf_counter() - t0) / 13 * 1e3, 4)}),
+              flush=True)
+        return
 
     if args.chain_only:
         st.build_chain()
