@@ -37,6 +37,9 @@ _SIGS = {
     "orc_residual_add": (None, [_p, _p, _i64]),
     "orc_silu_mul_quant": (None, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i]),
     "orc_gemm_fp16_exact": (None, [_p, _p, _p, _p, _i, _i, _i]),
+    "orc_qkv_split_gqa": (None, [_p, _p, _p, _p, _i, _i, _i, _i]),
+    "orc_merge_heads": (None, [_p, _p, _i, _i, _i]),
+    "orc_prefill_attention": (None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]),
     "orc_num_threads": (_i, []),
     "orc_set_num_threads": (None, [_i]),
 }
@@ -230,6 +233,56 @@ def fp16_linear_tolerance(y_exact, abs_sum):
     y16 = np.abs(y_exact).astype(np.float16)
     ulp = np.spacing(y16).astype(np.float64)
     return np.maximum(ulp, 1e-3 * np.abs(y_exact)) + abs_sum * 2.0 ** -18
+
+
+def qkv_split_gqa(qkv, n_q, n_kv, D):
+    """Token-major fused QKV [T, (n_q + 2 n_kv) D] -> q [n_q, T, D],
+    k [n_kv, T, D], v [n_kv, T, D] (prefill_attention.cu:38-57)."""
+    qkv = _c(qkv, np.float16)
+    T = qkv.shape[0]
+    q = np.empty((n_q, T, D), np.float16)
+    k = np.empty((n_kv, T, D), np.float16)
+    v = np.empty((n_kv, T, D), np.float16)
+    lib().orc_qkv_split_gqa(_ptr(qkv), _ptr(q), _ptr(k), _ptr(v), T, n_q, n_kv, D)
+    return q, k, v
+
+
+def merge_heads(heads):
+    """Head-major [H, T, D] -> token-major [T, H * D] (prefill_attention.cu:68-86)."""
+    heads = _c(heads, np.float16)
+    H, T, D = heads.shape
+    out = np.empty((T, H * D), np.float16)
+    lib().orc_merge_heads(_ptr(heads), _ptr(out), T, H, D)
+    return out
+
+
+def prefill_attention(q, k, v, sm_scale, window=0):
+    """Causal GQA attention over head-major fp16 q [n_q, T, D], k / v
+    [n_kv, T, D] (prefill_attention.cu:226-349).  Returns (out [n_q, T, D]
+    fp16, sum_j P_ij |V_jd| float64) -- the second scales the tolerance."""
+    q = _c(q, np.float16)
+    k = _c(k, np.float16)
+    v = _c(v, np.float16)
+    n_q, T, D = q.shape
+    n_kv = k.shape[0]
+    assert k.shape == (n_kv, T, D) and v.shape == k.shape and n_q % n_kv == 0
+    out = np.empty((n_q, T, D), np.float16)
+    aw = np.empty((n_q, T, D), np.float64)
+    lib().orc_prefill_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(aw), n_q, n_kv, T,
+                                D, float(sm_scale), int(window))
+    return out, aw
+
+
+def attention_tolerance(o_ref, absw):
+    """Allowed |o - o_ref| for a different (valid) evaluation order of the
+    reference's attention: two fp16 ulps of the output (the reference rounds
+    O once, a second evaluation may land one ulp away, plus one for the
+    scores' and probabilities' own fp16 roundings reaching the output) and
+    4e-3 of sum_j P_ij |V_jd| for the fp16 rounding of P (2^-11 relative,
+    doubled for a one-ulp difference in a score feeding exp)."""
+    o = np.abs(o_ref.astype(np.float64))
+    ulp = np.spacing(np.abs(o_ref).astype(np.float16)).astype(np.float64)
+    return 2.0 * ulp + 1e-3 * o + 4e-3 * absw
 
 
 def rms_inv(sum_sq, dim, eps):

@@ -30,6 +30,13 @@
  *                                (tests/test_kernels.cu:354-481) plus float64.
  *   orc_gemm_fp16_exact          exact rational sums (Python fractions) on
  *                                small inputs and one-hot closed forms.
+ *   orc_qkv_split_gqa / orc_merge_heads  numpy slicing / transposition of the
+ *                                same layouts (independent index algebra).
+ *   orc_prefill_attention        closed forms (T = 1 -> V row 0; Q = 0 -> the
+ *                                mean of V over the causal/window range;
+ *                                window 1 -> V row i), a float64 softmax
+ *                                evaluation within the stated tolerance, and
+ *                                a swapped K/V or a broken mask shown to fail.
  * The reference's CUDA intrinsics rsqrtf/expf are approximations whose
  * constants are not reproduced: this oracle uses (float)(1/sqrt(double)) and
  * (float)exp(double) instead, and the device code uses the same formulas.
@@ -386,6 +393,104 @@ void orc_silu_mul_quant(const uint16_t* gate, const uint16_t* up,
     orc_mul(h, up, n);
     orc_quantize_activations(h, act_scale, smooth_inv, n_tokens, dim, group_size, x_q, x_scale);
     if (!out_f16) free(h);
+}
+
+
+/* ------------------------------------------------- prefill attention ---- */
+
+/* qkv_split_gqa_kernel (src/kernels/prefill_attention.cu:38-57): token-major
+ * fused QKV [T, (n_q + 2 n_kv) D] -> head-major q [n_q, T, D], k / v
+ * [n_kv, T, D]. */
+void orc_qkv_split_gqa(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                       int n_q, int n_kv, int D) {
+    const int64_t stride = (int64_t)(n_q + 2 * n_kv) * D;
+    for (int t = 0; t < T; ++t) {
+        const uint16_t* row = qkv + (int64_t)t * stride;
+        for (int h = 0; h < n_q; ++h)
+            memcpy(q + ((int64_t)h * T + t) * D, row + (int64_t)h * D, (size_t)D * 2);
+        for (int h = 0; h < n_kv; ++h) {
+            memcpy(k + ((int64_t)h * T + t) * D, row + (int64_t)(n_q + h) * D, (size_t)D * 2);
+            memcpy(v + ((int64_t)h * T + t) * D, row + (int64_t)(n_q + n_kv + h) * D,
+                   (size_t)D * 2);
+        }
+    }
+}
+
+/* merge_heads_kernel (prefill_attention.cu:68-86): head-major [H, T, D] ->
+ * token-major [T, H * D]. */
+void orc_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D) {
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < H; ++h)
+            memcpy(out + ((int64_t)t * H + h) * D, heads + ((int64_t)h * T + t) * D,
+                   (size_t)D * 2);
+}
+
+/* prefill_attention_gpu (src/kernels/prefill_attention.cu:226-322) with its stages:
+ *   1. S = Q K^T per head (cublasGemmStridedBatchedEx, fp32 compute, fp16
+ *      scores); query head h reads kv head h / (n_q / n_kv)
+ *      (gqa_expand_kernel, :118-139).  cuBLAS's summation order is
+ *      unspecified; here the fp32 sum runs over d = 0 .. D-1 with FMAs.
+ *   2. causal_softmax_kernel (:141-224): v = float(S) * sm_scale for
+ *      left <= j <= i (left = i - window + 1 when window > 0, else 0), else
+ *      -1e30; mx = max; e = exp(v - mx); sum; P = half(e * (1 / sum)).  exp is
+ *      (float)exp(double) and the sum runs in j order (the reference's tree
+ *      order is a rounding detail inside the stated tolerance).
+ *   3. sgemv_kernel (:325-349): O[i, d] = half(sum_j float(P_ij) * float(V_jd)),
+ *      j in order, nvcc contracts into an FMA chain.
+ * absw, when non-null, receives sum_j float(P_ij) * |float(V_jd)| (float64)
+ * per output, the scale of the tolerance the tests apply. */
+void orc_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           uint16_t* out, double* absw, int n_q, int n_kv, int T, int D,
+                           float sm_scale, int window) {
+    const int gs = n_q / n_kv;
+    #pragma omp parallel
+    {
+        float* qr = (float*)malloc(sizeof(float) * (size_t)D);
+        float* srow = (float*)malloc(sizeof(float) * (size_t)T);
+        uint16_t* prow = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T);
+        #pragma omp for schedule(dynamic) collapse(2)
+        for (int h = 0; h < n_q; ++h)
+            for (int i = 0; i < T; ++i) {
+                const uint16_t* Kh = k + (int64_t)(h / gs) * T * D;
+                const uint16_t* Vh = v + (int64_t)(h / gs) * T * D;
+                const uint16_t* Qi = q + ((int64_t)h * T + i) * D;
+                for (int d = 0; d < D; ++d) qr[d] = orc_h2f(Qi[d]);
+                const int left = window > 0 ? i - window + 1 : 0;
+                float mx = -1e30f;
+                for (int j = 0; j < T; ++j) {
+                    float acc = 0.0f;
+                    const uint16_t* Kj = Kh + (int64_t)j * D;
+                    for (int d = 0; d < D; ++d) acc = fmaf(qr[d], orc_h2f(Kj[d]), acc);
+                    float val = orc_h2f(orc_f2h(acc));
+                    val = (j <= i && j >= left) ? val * sm_scale : -1e30f;
+                    srow[j] = val;
+                    if (val > mx) mx = val;
+                }
+                float sum = 0.0f;
+                for (int j = 0; j < T; ++j) {
+                    const float e = (float)exp((double)(srow[j] - mx));
+                    srow[j] = e;
+                    sum += e;
+                }
+                const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+                for (int j = 0; j < T; ++j) prow[j] = orc_f2h(srow[j] * inv);
+                for (int d = 0; d < D; ++d) {
+                    float acc = 0.0f;
+                    double aw = 0.0;
+                    for (int j = 0; j < T; ++j) {
+                        const float pj = orc_h2f(prow[j]);
+                        const float vj = orc_h2f(Vh[(int64_t)j * D + d]);
+                        acc = fmaf(pj, vj, acc);   /* nvcc contracts */
+                        aw += (double)pj * fabs((double)vj);
+                    }
+                    out[((int64_t)h * T + i) * D + d] = orc_f2h(acc);
+                    if (absw) absw[((int64_t)h * T + i) * D + d] = aw;
+                }
+            }
+        free(qr);
+        free(srow);
+        free(prow);
+    }
 }
 
 /* ------------------------------------------------------------ threads ---- */

@@ -100,6 +100,13 @@ int orc_num_threads(void);
 void orc_set_num_threads(int n);
 
 /* fp16 linear as an exact value: Y, sum|w x| [N, M] in double. */
+/* Prefill attention side (src/kernels/prefill_attention.cu). */
+void orc_qkv_split_gqa(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                       int n_q, int n_kv, int D);
+void orc_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D);
+void orc_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           uint16_t* out, double* absw, int n_q, int n_kv, int T, int D,
+                           float sm_scale, int window);
 void orc_gemm_fp16_exact(const uint16_t* W, const uint16_t* X, double* Y, double* absY,
                          int M, int N, int K);
 

@@ -324,3 +324,94 @@ def test_gemm_fp16_exact_rational():
     assert np.array_equal(Y1, X[:, [0, 2, 4, 6]].astype(np.float64))
     # a transposed operand or a swapped output index fails
     assert not np.allclose(ref.gemm_fp16_exact(W, X)[0], ref.gemm_fp16_exact(W, X)[0][:, ::-1])
+
+
+# ------------------------------------------------------- prefill attention ---
+
+def _qkv(rng, T, n_q, n_kv, D, scale=1.0):
+    return (rng.standard_normal((T, (n_q + 2 * n_kv) * D)) * scale).astype(np.float16)
+
+
+def test_qkv_split_and_merge_index_algebra():
+    rng = np.random.default_rng(11)
+    n_q, n_kv, T, D = 6, 2, 19, 32
+    qkv = _qkv(rng, T, n_q, n_kv, D)
+    q, k, v = ref.qkv_split_gqa(qkv, n_q, n_kv, D)
+    heads = qkv.reshape(T, n_q + 2 * n_kv, D).transpose(1, 0, 2)
+    assert np.array_equal(q, heads[:n_q])
+    assert np.array_equal(k, heads[n_q:n_q + n_kv])
+    assert np.array_equal(v, heads[n_q + n_kv:])
+    # merge_heads inverts the q split; swapping T and H in merge would fail this
+    assert np.array_equal(ref.merge_heads(q), qkv[:, :n_q * D])
+
+
+def _attention_f64(q, k, v, sm_scale, window):
+    n_q, T, D = q.shape
+    rep = n_q // k.shape[0]
+    kk = np.repeat(k, rep, 0).astype(np.float64)
+    vv = np.repeat(v, rep, 0).astype(np.float64)
+    S = np.einsum("htd,hsd->hts", q.astype(np.float64), kk) * sm_scale
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    mask = j <= i
+    if window > 0:
+        mask &= j >= i - window + 1
+    S = np.where(mask, S, -np.inf)
+    P = np.exp(S - S.max(-1, keepdims=True))
+    P /= P.sum(-1, keepdims=True)
+    return P @ vv
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(12)
+    n_q, n_kv, T, D = 4, 2, 23, 64
+    q, k, v = ref.qkv_split_gqa(_qkv(rng, T, n_q, n_kv, D), n_q, n_kv, D)
+    rep = n_q // n_kv
+    vq = np.repeat(v, rep, 0)
+    # T = 1: the only key is row 0, P = 1 exactly
+    o1, _ = ref.prefill_attention(q[:, :1], k[:, :1], v[:, :1], 0.125)
+    assert np.array_equal(o1, vq[:, :1])
+    # window 1: every query sees only itself
+    ow, _ = ref.prefill_attention(q, k, v, 0.125, window=1)
+    assert np.array_equal(ow, vq)
+    # Q = 0: uniform weights over the causal prefix (window 4: the last 4)
+    z = np.zeros_like(q)
+    for win in (0, 4):
+        oz, _ = ref.prefill_attention(z, k, v, 0.125, window=win)
+        want = np.empty(oz.shape)
+        for i in range(T):
+            lo = max(0, i - win + 1) if win else 0
+            want[:, i] = vq[:, lo:i + 1].astype(np.float64).mean(1)
+        # P = half(1/n) carries up to 2^-11 relative error per weight
+        assert np.all(np.abs(oz - want) <= 2 * fp16_ulp(want) + 1e-3 * np.abs(vq).max())
+
+
+@pytest.mark.parametrize("n_q,n_kv,T,D,win", [(4, 2, 37, 64, 0), (8, 2, 64, 128, 0),
+                                               (4, 4, 50, 64, 7), (2, 1, 130, 32, 0)])
+def test_attention_against_float64(n_q, n_kv, T, D, win):
+    rng = np.random.default_rng(13 + T)
+    q, k, v = ref.qkv_split_gqa(_qkv(rng, T, n_q, n_kv, D), n_q, n_kv, D)
+    s = 1.0 / np.sqrt(D)
+    o, aw = ref.prefill_attention(q, k, v, s, window=win)
+    want = _attention_f64(q, k, v, s, win)
+    assert np.all(np.abs(o - want) <= ref.attention_tolerance(want, aw))
+
+
+def test_attention_tolerance_rejects_plausible_mistakes():
+    rng = np.random.default_rng(14)
+    n_q, n_kv, T, D = 4, 2, 40, 64
+    q, k, v = ref.qkv_split_gqa(_qkv(rng, T, n_q, n_kv, D, 2.0), n_q, n_kv, D)
+    s = 1.0 / np.sqrt(D)
+    want = _attention_f64(q, k, v, s, 0)
+    _, aw = ref.prefill_attention(q, k, v, s)
+    tol = ref.attention_tolerance(want, aw)
+    # K and V swapped, a non-causal mask, a wrong kv head mapping, no scale
+    nc = np.einsum("htd,hsd->hts", q.astype(np.float64), np.repeat(k, 2, 0).astype(np.float64)) * s
+    P = np.exp(nc - nc.max(-1, keepdims=True))
+    P /= P.sum(-1, keepdims=True)
+    bad = [ref.prefill_attention(q, v, k, s)[0],
+           (P @ np.repeat(v, 2, 0).astype(np.float64)).astype(np.float16),
+           ref.prefill_attention(q, k[::-1].copy(), v[::-1].copy(), s)[0],
+           ref.prefill_attention(q, k, v, 1.0)[0]]
+    for b in bad:
+        assert np.any(np.abs(b - want) > tol)
