@@ -29,6 +29,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+FP16_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA
 METRIC = "decode GEMV HBM GB/s + prefill INT8 TOPS (% of MI355X peak), g256/g64"
 
 
@@ -85,6 +86,8 @@ def main():
                          "(for rocprofv3 runs)")
     ap.add_argument("--chain-only", action="store_true",
                     help="only the configs[4] decode chain, 20 runs (for rocprofv3 runs)")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="only the T=2048 prefill attention side (for rocprofv3 runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configs[3] M=2048 g256 prefill GEMMs (for rocprofv3 runs)")
     args = ap.parse_args()
@@ -99,6 +102,9 @@ def main():
     from fish_amd.synth import LAYER_SHAPES
 
     torch.cuda.init()
+    if args.attn_only:
+        print(json.dumps(attention_side(torch, ops)), flush=True)
+        return
     if args.prefill_only:
         print(json.dumps(prefill_tops(torch, ops, [(256, 2048)])), flush=True)
         return
@@ -315,6 +321,35 @@ def run_secondary(torch, ops, st, args):
 
     # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
     out.update(prefill_tops(torch, ops, [(256, 512), (256, 2048), (64, 2048)]))
+    out.update(attention_side(torch, ops))
+    return out
+
+
+def attention_side(torch, ops):
+    """The prefill attention side at the DualAR shape (n_q 32, n_kv 8, D 128,
+    dual_ar_config.h:11-15), T = 2048: fused QKV split, causal attention,
+    head merge.  Attention FLOPs count the causal half only:
+    4 D n_q T (T + 1) / 2 (QK^T and PV, 2 flops per multiply-add)."""
+    T, n_q, n_kv, D = 2048, 32, 8, 128
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    qkv = torch.randn((T, (n_q + 2 * n_kv) * D), generator=gen, device="cuda").half()
+    q, k, v = ops.qkv_split_heads_gqa(qkv, n_q, n_kv, D)
+    o = torch.empty_like(q)
+    m = torch.empty((T, n_q * D), device="cuda", dtype=torch.float16)
+    sc = 1.0 / D ** 0.5
+    out = {}
+    us = graph_us_per_call(torch, [lambda: ops.prefill_attention(q, k, v, sc, out=o)] * 4, reps=5)
+    fl = 4.0 * D * n_q * T * (T + 1) / 2
+    out["prefill_attn_t2048_us"] = round(us, 2)
+    out["prefill_attn_t2048_TFLOPs"] = round(fl / (us * 1e-6) / 1e12, 1)
+    out["prefill_attn_t2048_frac_fp16_peak"] = round(fl / (us * 1e-6) / 1e12 / FP16_PEAK_TFLOPS, 4)
+    us = graph_us_per_call(torch, [lambda: ops.qkv_split_heads_gqa(qkv, n_q, n_kv, D)] * 4)
+    out["qkv_split_t2048_us"] = round(us, 2)
+    out["qkv_split_t2048_GBs"] = round(2 * qkv.numel() * 2 / (us * 1e-6) / 1e9, 1)
+    us = graph_us_per_call(torch, [lambda: ops.merge_heads(o, out=m)] * 4)
+    out["merge_heads_t2048_us"] = round(us, 2)
+    out["merge_heads_t2048_GBs"] = round(2 * o.numel() * 2 / (us * 1e-6) / 1e9, 1)
     return out
 
 

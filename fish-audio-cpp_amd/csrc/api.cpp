@@ -508,6 +508,68 @@ int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, in
     return FA_OK;
 }
 
+int fa_qkv_split_heads_gqa(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                           int n_q, int n_kv, int head_dim, void* stream) {
+    const char* fn = "fa_qkv_split_heads_gqa";
+    g_err.clear();
+    if (T < 0 || n_q <= 0 || n_kv <= 0 || head_dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad T=%d n_q=%d n_kv=%d head_dim=%d", fn, T, n_q,
+                    n_kv, head_dim);
+    if ((int64_t)T * (n_q + 2 * n_kv) * head_dim > INT32_MAX)
+        return fail(FA_ERR_INVALID_ARG, "%s: qkv larger than 2^31 elements", fn);
+    if (T == 0) return FA_OK;
+    if (!qkv || !q || !k || !v) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    const bool vec = head_dim % 8 == 0 && aligned16(qkv) && aligned16(q) && aligned16(k) &&
+                     aligned16(v);
+    FA_HIP(fa::launch_qkv_split(qkv, q, k, v, T, n_q, n_kv, head_dim, vec, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_qkv_split_heads(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                       int n_heads, int head_dim, void* stream) {
+    return fa_qkv_split_heads_gqa(qkv, q, k, v, T, n_heads, n_heads, head_dim, stream);
+}
+
+int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int head_dim,
+                   void* stream) {
+    const char* fn = "fa_merge_heads";
+    g_err.clear();
+    if (T < 0 || n_heads <= 0 || head_dim <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad T=%d n_heads=%d head_dim=%d", fn, T, n_heads,
+                    head_dim);
+    if ((int64_t)T * n_heads * head_dim > INT32_MAX)
+        return fail(FA_ERR_INVALID_ARG, "%s: more than 2^31 elements", fn);
+    if (T == 0) return FA_OK;
+    if (!heads || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    const bool vec = head_dim % 8 == 0 && aligned16(heads) && aligned16(out);
+    FA_HIP(fa::launch_merge_heads(heads, out, T, n_heads, head_dim, vec, (hipStream_t)stream));
+    return FA_OK;
+}
+
+int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                         void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
+                         void* stream, int window_size) {
+    const char* fn = "fa_prefill_attention";
+    (void)workspace;   // the fused kernel keeps scores on chip
+    g_err.clear();
+    if (T < 0 || n_q <= 0 || n_kv <= 0 || D <= 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: bad n_q=%d n_kv=%d T=%d D=%d", fn, n_q, n_kv, T, D);
+    if (n_q % n_kv != 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: n_q=%d is not a multiple of n_kv=%d", fn, n_q, n_kv);
+    if (D % 8 != 0 || fa::attention_padded_dim(D) == 0)
+        return fail(FA_ERR_INVALID_ARG, "%s: head dim %d unsupported (D %% 8 == 0, D <= 128)", fn,
+                    D);
+    if ((int64_t)n_q * T * D > INT32_MAX)
+        return fail(FA_ERR_INVALID_ARG, "%s: q larger than 2^31 elements", fn);
+    if (T == 0) return FA_OK;
+    if (!q || !k || !v || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 16-byte aligned", fn);
+    FA_HIP(fa::launch_prefill_attention(q, k, v, out, n_q, n_kv, T, D, sm_scale, window_size,
+                                        (hipStream_t)stream));
+    return FA_OK;
+}
+
 int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_size, void* stream) {
     const char* fn = "fa_workspace_reserve";
     g_err.clear();

@@ -1,0 +1,319 @@
+// attn.hip -- prefill-side neighbours of the W8A8 linears: the fused-QKV head
+// split, the head merge and causal (optionally windowed) GQA attention.
+//
+// Reference: src/kernels/prefill_attention.cu.  The reference materialises the
+// fp16 score matrix S = Q K^T [n_q, T, T] with a batched GEMM, runs a masked
+// row softmax in place and a per-row S V product.  Here one kernel keeps a
+// 32-query tile of each of the group's query heads on chip and streams 32-key
+// blocks of K and V through LDS, with the running-max (online) softmax, so the
+// T x T matrix never reaches HBM.  Numerics follow the reference where they
+// are observable: every score is rounded to fp16 before it is scaled
+// (prefill_attention.cu:276-290 writes S in fp16, :160-162 reads it back),
+// masked keys get weight 0, probabilities enter the V product as fp16 and the
+// V product accumulates in fp32.  Only the order of fp32 sums and the point at
+// which the weights are normalised (here after the V product, there before)
+// differ; the tests bound the effect.
+//
+// Matrix-core mapping (v_mfma_f32_32x32x16_f16, one wave = 32 queries):
+//   S^T[key][query] = K Q^T      A = K block from LDS   (row key,  k = d)
+//                                B = Q tile, registers  (col query, k = d)
+//   O^T[d][query]  += V^T P^T    A = V^T block from LDS (row d,    k = key)
+//                                B = P^T, registers     (col query, k = key)
+// For an A/B operand, lane l holds row/column l % 32 and k = 8 (l / 32) + 0..7;
+// accumulator element i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4,
+// column l % 32.  So after the score MFMAs each lane owns 16 keys of one
+// query; its elements 0..7 and 8..15 are exactly the k slots the P^T operand
+// needs for keys 0..15 and 16..31, with slot 8h + t <-> key
+// 4h + t (t < 4) or 8 + 4h + (t - 4) (t >= 4).  The V^T operand is read from
+// LDS in that same key order, so no lane exchange is needed between the two
+// products; one lane swap (lane l <-> l ^ 32) gives the per-query maximum.
+#include "common.h"
+
+namespace fa {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+constexpr int kAttnWaves = 4;      // query heads of one KV group per workgroup
+constexpr int kAttnTile = 32;      // queries per wave and keys per block
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kMasked = -1e30f;  // the reference's mask value (prefill_attention.cu:161)
+
+__device__ __forceinline__ h8 ld_h8(const uint16_t* p) {
+    return *reinterpret_cast<const h8*>(p);
+}
+
+// One workgroup: KV head `g`, query heads g * gs + chunk * 4 + wave, queries
+// q0 .. q0 + 31.  DP = head dim rounded up to 32 (D % 8 == 0, D <= DP).
+template <int DP>
+__global__ void __launch_bounds__(kAttnWaves * 64, 2)
+attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                 const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
+                 int T, int D, float sm_scale, int window, int chunks, int n_qb) {
+    constexpr int KS = DP + 8;            // K row stride in LDS (halves)
+    constexpr int VS = kAttnTile + 4;     // V^T row stride in LDS (halves)
+    constexpr int NC = 4 * DP;            // 16-byte chunks per 32-key block of K (and of V)
+    constexpr int PT = (NC + kAttnWaves * 64 - 1) / (kAttnWaves * 64);
+    constexpr int NKK = DP / 16;          // score MFMAs per block
+    constexpr int NDB = DP / 32;          // d blocks of O^T
+    __shared__ __align__(16) uint16_t Ks[kAttnTile * KS];
+    __shared__ __align__(16) uint16_t Vt[DP * VS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
+    const int gs = n_q / n_kv;
+    // heaviest (last) query tiles first: they have the most key blocks
+    const int qb = n_qb - 1 - (int)(blockIdx.x / (n_kv * chunks));
+    const int rest = (int)(blockIdx.x % (n_kv * chunks));
+    const int g = rest % n_kv, chunk = rest / n_kv;
+    const int hq = chunk * kAttnWaves + wave;        // head index within the group
+    const bool active = hq < gs;
+    const int head = g * gs + (active ? hq : 0);
+    const int q0 = qb * kAttnTile;
+    const int qi = q0 + col;                         // this lane's query
+
+    const uint16_t* Kg = k + (int64_t)g * T * D;
+    const uint16_t* Vg = v + (int64_t)g * T * D;
+
+    // Q tile (B operand of the score product), zero past D and past T.
+    h8 qf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        const int d = 16 * kk + 8 * hh;
+        if (qi < T && d < D)
+            qf[kk] = ld_h8(q + ((int64_t)head * T + qi) * D + d);
+        else
+            qf[kk] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+
+    const int hi = min(T - 1, q0 + kAttnTile - 1);
+    const int lo = window > 0 ? max(0, q0 - window + 1) : 0;
+    const int kb_lo = lo / kAttnTile, kb_hi = hi / kAttnTile;
+    const int left = window > 0 ? qi - window + 1 : 0;   // this lane's first key
+
+    // Block loads: chunk c -> key c % 32, d 8 (c / 32); lanes of a wave run
+    // over keys so the transposed V writes spread over LDS banks.
+    h8 kr[PT], vr[PT];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+            const int c = tid + p * kAttnWaves * 64;
+            const int key = kb * kAttnTile + (c & 31), d = 8 * (c >> 5);
+            const bool ok = c < NC && key < T && d < D;
+            kr[p] = ok ? ld_h8(Kg + (int64_t)key * D + d) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            vr[p] = ok ? ld_h8(Vg + (int64_t)key * D + d) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    };
+    auto store_block = [&]() {
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+            const int c = tid + p * kAttnWaves * 64;
+            if (c < NC) {
+                const int key = c & 31, d = 8 * (c >> 5);
+                *reinterpret_cast<h8*>(&Ks[key * KS + d]) = kr[p];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    _Float16 x = vr[p][e];
+                    Vt[(d + e) * VS + key] = __builtin_bit_cast(uint16_t, x);
+                }
+            }
+        }
+    };
+
+    f16x acc_o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc_o[db][i] = 0.0f;
+    float m_run = kMasked, l_run = 0.0f;
+
+    load_block(kb_lo);
+    for (int kb = kb_lo; kb <= kb_hi; ++kb) {
+        __syncthreads();                 // previous block's LDS reads are done
+        store_block();
+        __syncthreads();
+        if (kb < kb_hi) load_block(kb + 1);
+        if (!active) continue;
+
+        // S^T = K Q^T
+        f16x s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            const h8 a = *reinterpret_cast<const h8*>(&Ks[col * KS + 16 * kk + 8 * hh]);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s, 0, 0, 0);
+        }
+
+        // mask, scale (score rounded to fp16 first), running max
+        const int kbase = kb * kAttnTile + 4 * hh;
+        float mloc = kMasked;
+        bool ok[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int j = kbase + 8 * (i >> 2) + (i & 3);
+            ok[i] = j <= qi && j >= left;
+            const float x = h2f(f2h(s[i])) * sm_scale;
+            s[i] = x;
+            mloc = ok[i] ? fmaxf(mloc, x) : mloc;
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = exp2f((m_run - m_new) * kLog2e);
+        m_run = m_new;
+
+        h8 pb[2];
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float e = ok[i] ? exp2f((s[i] - m_new) * kLog2e) : 0.0f;
+            const _Float16 e16 = (_Float16)e;
+            lsum += (float)e16;
+            pb[i >> 3][i & 7] = e16;
+        }
+        l_run = l_run * alpha + lsum;
+
+        // O^T = alpha O^T + V^T P^T
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc_o[db][i] *= alpha;
+            const uint16_t* vrow = &Vt[(32 * db + col) * VS + 4 * hh];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const h4 a0 = *reinterpret_cast<const h4*>(vrow + 16 * k2);
+                const h4 a1 = *reinterpret_cast<const h4*>(vrow + 16 * k2 + 8);
+                const h8 a = h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[k2], acc_o[db], 0, 0, 0);
+            }
+        }
+    }
+
+    if (!active || qi >= T) return;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* orow = out + ((int64_t)head * T + qi) * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = 32 * db + 8 * r + 4 * hh;
+            if (d < D) {
+                uint16_t o4[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o4[t] = f2h(acc_o[db][4 * r + t] * inv);
+                uint2 w;
+                w.x = (uint32_t)o4[0] | ((uint32_t)o4[1] << 16);
+                w.y = (uint32_t)o4[2] | ((uint32_t)o4[3] << 16);
+                *reinterpret_cast<uint2*>(orow + d) = w;
+            }
+        }
+}
+
+// Fused QKV [T, (n_q + 2 n_kv) D] -> q [n_q, T, D], k / v [n_kv, T, D]; one
+// thread per VEC halves (VEC = 8 when D % 8 == 0 and every buffer is 16-byte
+// aligned, else 1).
+template <int VEC>
+__global__ void qkv_split_kernel(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ q,
+                                 uint16_t* __restrict__ k, uint16_t* __restrict__ v, int T,
+                                 int n_q, int n_kv, int D) {
+    typedef uint16_t u16v __attribute__((ext_vector_type(VEC)));
+    const int DV = D / VEC;
+    const int64_t total = (int64_t)T * (n_q + 2 * n_kv) * DV;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    // source order: consecutive threads read consecutive chunks of one token row
+    const int dv = (int)(idx % DV);
+    const int64_t r = idx / DV;
+    const int slot = (int)(r % (n_q + 2 * n_kv));
+    const int t = (int)(r / (n_q + 2 * n_kv));
+    const u16v x = *reinterpret_cast<const u16v*>(qkv + idx * VEC);
+    uint16_t* dst;
+    if (slot < n_q)
+        dst = q + ((int64_t)slot * T + t) * D;
+    else if (slot < n_q + n_kv)
+        dst = k + ((int64_t)(slot - n_q) * T + t) * D;
+    else
+        dst = v + ((int64_t)(slot - n_q - n_kv) * T + t) * D;
+    *reinterpret_cast<u16v*>(dst + dv * VEC) = x;
+}
+
+// Head-major [H, T, D] -> token-major [T, H D].
+template <int VEC>
+__global__ void merge_heads_kernel(const uint16_t* __restrict__ heads, uint16_t* __restrict__ out,
+                                   int T, int H, int D) {
+    typedef uint16_t u16v __attribute__((ext_vector_type(VEC)));
+    const int DV = D / VEC;
+    const int64_t total = (int64_t)T * H * DV;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    // destination order: consecutive threads write consecutive chunks of a token row
+    const int dv = (int)(idx % DV);
+    const int64_t r = idx / DV;
+    const int h = (int)(r % H);
+    const int t = (int)(r / H);
+    *reinterpret_cast<u16v*>(out + idx * VEC) =
+        *reinterpret_cast<const u16v*>(heads + ((int64_t)h * T + t) * D + dv * VEC);
+}
+
+inline unsigned blocks_for(int64_t n, int threads) {
+    return (unsigned)((n + threads - 1) / threads);
+}
+
+}  // namespace
+
+int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
+
+hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                    int window, hipStream_t stream) {
+    const int gs = n_q / n_kv;
+    const int chunks = (gs + kAttnWaves - 1) / kAttnWaves;
+    const int n_qb = (T + kAttnTile - 1) / kAttnTile;
+    const dim3 grid((unsigned)(n_qb * n_kv * chunks)), block(kAttnWaves * 64);
+    switch (attention_padded_dim(D)) {
+        case 32:
+            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                             sm_scale, window, chunks, n_qb);
+            break;
+        case 64:
+            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                             sm_scale, window, chunks, n_qb);
+            break;
+        case 128:
+            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                              sm_scale, window, chunks, n_qb);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_split(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                            int n_q, int n_kv, int D, bool vec, hipStream_t stream) {
+    const int64_t rows = (int64_t)T * (n_q + 2 * n_kv);
+    if (vec)
+        qkv_split_kernel<8><<<blocks_for(rows * (D / 8), 256), 256, 0, stream>>>(qkv, q, k, v, T,
+                                                                               n_q, n_kv, D);
+    else
+        qkv_split_kernel<1><<<blocks_for(rows * D, 256), 256, 0, stream>>>(qkv, q, k, v, T, n_q,
+                                                                         n_kv, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D, bool vec,
+                              hipStream_t stream) {
+    const int64_t rows = (int64_t)T * H;
+    if (vec)
+        merge_heads_kernel<8><<<blocks_for(rows * (D / 8), 256), 256, 0, stream>>>(heads, out, T,
+                                                                                 H, D);
+    else
+        merge_heads_kernel<1><<<blocks_for(rows * D, 256), 256, 0, stream>>>(heads, out, T, H, D);
+    return hipGetLastError();
+}
+
+}  // namespace fa

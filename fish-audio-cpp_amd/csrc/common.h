@@ -204,6 +204,17 @@ hipError_t launch_gemv_f16(const uint16_t* W, const uint16_t* X, uint16_t* Y, in
 hipError_t launch_gemm_f16_generic(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N,
                                    int K, hipStream_t stream);
 
+// Prefill attention side (attn.hip).  attention_padded_dim gives the head dim
+// the fused attention kernel is instantiated for (32, 64 or 128), 0 if D > 128.
+int attention_padded_dim(int D);
+hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                    uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                    int window, hipStream_t stream);
+hipError_t launch_qkv_split(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                            int n_q, int n_kv, int D, bool vec, hipStream_t stream);
+hipError_t launch_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D, bool vec,
+                              hipStream_t stream);
+
 // Any-shape fallback (any K, any group size, unaligned pointers).
 hipError_t launch_gemm_generic(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                                const float* x_scale, uint16_t* Y, int32_t* dbg_partials,

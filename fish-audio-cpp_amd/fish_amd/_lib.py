@@ -83,6 +83,10 @@ SIGNATURES = {
     "fa_residual_add": (_i, [_p, _p, _i64, _p]),
     "fa_silu_mul_quant": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _p]),
     "fa_quantize_weights_groupwise": (_i, [_p, _i64, _i64, _i, _p, _p, _p]),
+    "fa_qkv_split_heads_gqa": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "fa_qkv_split_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_merge_heads": (_i, [_p, _p, _i, _i, _i, _p]),
+    "fa_prefill_attention": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i]),
     "fa_workspace_reserve": (_i, [_i, _i, _i, _i, _p]),
     "fa_workspace_release": (_i, []),
     "fa_chain_create": (_i, [ctypes.POINTER(ChainStep), _i, _i, ctypes.POINTER(_p)]),

@@ -30,7 +30,7 @@ HIP_FLAGS = [
 ]
 
 HIP_SOURCES = ["quant.hip", "gemv.hip", "gemv_dot.hip", "gemv_dot_pro.hip", "gemv_dot_swiglu.hip",
-               "gemv_f16.hip", "gemm.hip", "chain.hip"]
+               "gemv_f16.hip", "gemm.hip", "chain.hip", "attn.hip"]
 HOST_SOURCES = ["api.cpp", "loader.cpp", "kernels_cxx.cpp"]
 
 

@@ -223,6 +223,44 @@ def quantize_weights_groupwise(w, group_size):
     return q, s
 
 
+def qkv_split_heads_gqa(qkv, n_q, n_kv, head_dim):
+    """qkv fp16 [T, (n_q + 2 n_kv) head_dim] -> head-major (q, k, v)
+    (prefill_attention.cu:38-66)."""
+    _need(qkv, torch.float16, "qkv")
+    T = qkv.shape[0]
+    assert qkv.shape[1] == (n_q + 2 * n_kv) * head_dim
+    q = torch.empty((n_q, T, head_dim), dtype=torch.float16, device=qkv.device)
+    k = torch.empty((n_kv, T, head_dim), dtype=torch.float16, device=qkv.device)
+    v = torch.empty_like(k)
+    check(lib().fa_qkv_split_heads_gqa(_ptr(qkv), _ptr(q), _ptr(k), _ptr(v), T, n_q, n_kv,
+                                       head_dim, _stream()))
+    return q, k, v
+
+
+def merge_heads(heads, out=None):
+    """Head-major fp16 [H, T, D] -> token-major [T, H D] (prefill_attention.cu:68-86)."""
+    _need(heads, torch.float16, "heads")
+    H, T, D = heads.shape
+    if out is None:
+        out = torch.empty((T, H * D), dtype=torch.float16, device=heads.device)
+    check(lib().fa_merge_heads(_ptr(heads), _ptr(out), T, H, D, _stream()))
+    return out
+
+
+def prefill_attention(q, k, v, sm_scale, window=0, out=None):
+    """Causal GQA attention, head-major fp16 q [n_q, T, D], k / v [n_kv, T, D]
+    (prefill_attention.cu:226-349) -> out [n_q, T, D]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, torch.float16, n)
+    n_q, T, D = q.shape
+    n_kv = k.shape[0]
+    if out is None:
+        out = torch.empty_like(q)
+    check(lib().fa_prefill_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), None, n_q, n_kv, T, D,
+                                     float(sm_scale), _stream(), int(window)))
+    return out
+
+
 class Chain:
     """fa_chain: one-token W8A8 linears run as one device-ordered launch.
 

@@ -179,6 +179,38 @@ int fa_quantize_weights_groupwise(const uint16_t* w, int64_t rows, int64_t K, in
                                   int8_t* q, uint16_t* scale, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Prefill attention side: the neighbours of the wqkv and wo linears.        */
+/* ------------------------------------------------------------------------ */
+
+/* fish::kernels::qkv_split_heads_gqa (src/kernels/kernels.h:338-341,
+ * prefill_attention.cu:38-66): fused QKV fp16 [T, (n_q + 2 n_kv) head_dim]
+ * (the wqkv output) -> head-major q [n_q, T, head_dim], k / v
+ * [n_kv, T, head_dim]. */
+int fa_qkv_split_heads_gqa(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                           int n_q, int n_kv, int head_dim, void* stream);
+/* fish::kernels::qkv_split_heads (kernels.h:335-336, prefill_attention.cu:14-36):
+ * the n_kv == n_heads case. */
+int fa_qkv_split_heads(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
+                       int n_heads, int head_dim, void* stream);
+/* fish::kernels::merge_heads (kernels.h:343-344, prefill_attention.cu:68-86):
+ * head-major [n_heads, T, head_dim] -> token-major [T, n_heads head_dim]
+ * (the wo input). */
+int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int head_dim,
+                   void* stream);
+/* fish::kernels::prefill_attention_gpu (kernels.h:324-333,
+ * prefill_attention.cu:226-349): causal GQA attention, query head h reading
+ * KV head h / (n_q / n_kv); window_size > 0 limits query i to keys
+ * i - window_size + 1 .. i.  q / out [n_q, T, D], k / v [n_kv, T, D], fp16,
+ * head-major, 16-byte aligned; D % 8 == 0 and D <= 128; n_q % n_kv == 0.
+ * One fused kernel: the T x T scores stay on chip, so `workspace` is not used
+ * (it may be NULL; the reference's cuBLAS handle has no counterpart).
+ * Results agree with the reference within the order of fp32 sums (scores are
+ * rounded to fp16 before scaling, probabilities enter the V product as fp16). */
+int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                         void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
+                         void* stream, int window_size);
+
+/* ------------------------------------------------------------------------ */
 /* Decode chain: a sequence of one-token W8A8 linears as one launch.          */
 /* ------------------------------------------------------------------------ */
 

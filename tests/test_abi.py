@@ -90,6 +90,19 @@ def test_invalid_arguments_rejected_without_device():
     assert l.fa_mul(dummy, None, 4, None) == 1
     assert l.fa_quantize_weights_groupwise(dummy, 4, 64, 0, dummy, dummy, None) == 1
     assert l.fa_quantize_activations(None, None, None, None, None, 1, 64, 64, None) == 1
+    # attention side: GQA ratio, head dim, alignment, empty sequence
+    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 6, 4, 8, 64, 0.1, None, 0) == 1
+    assert "multiple" in l.fa_last_error().decode()
+    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 136, 0.1, None,
+                                  0) == 1
+    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 60, 0.1, None, 0) == 1
+    odd = ctypes.c_void_p(18)
+    assert l.fa_prefill_attention(odd, dummy, dummy, dummy, None, 8, 4, 8, 64, 0.1, None, 0) == 1
+    assert "aligned" in l.fa_last_error().decode()
+    assert l.fa_prefill_attention(None, None, None, None, None, 8, 4, 0, 64, 0.1, None, 0) == 0
+    assert l.fa_qkv_split_heads_gqa(None, dummy, dummy, dummy, 4, 8, 4, 64, None) == 1
+    assert l.fa_qkv_split_heads(None, None, None, None, 0, 8, 64, None) == 0
+    assert l.fa_merge_heads(dummy, None, 4, 8, 64, None) == 1
     # a successful call clears the message
     assert l.fa_silu(None, 0, None) == 0
     assert l.fa_last_error().decode() == ""
