@@ -36,6 +36,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16x __attribute__((ext_vector_type(16)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kAttnWaves = 4;      // query heads of one KV group per workgroup
 constexpr int kAttnTile = 32;      // queries per wave and keys per block
@@ -46,21 +47,71 @@ __device__ __forceinline__ h8 ld_h8(const uint16_t* p) {
     return *reinterpret_cast<const h8*>(p);
 }
 
+// V^T key order: within each 16-key group, position p = 8h + t holds key
+// 4h + t (t < 4) or 8 + 4h + (t - 4) (t >= 4) -- the k-slot order of the P^T
+// operand -- so one 16-byte LDS read gives a lane its 8 V^T slots.
+__device__ __forceinline__ int vt_key(int p) {   // key offset (0..15) at position p
+    const int h = p >> 3, t = p & 7;
+    return t < 4 ? 4 * h + t : 8 + 4 * h + (t - 4);
+}
+
+// v [n_kv, T, D] -> vt [n_kv, D, Tp] (Tp = T rounded up to 32, zero past T),
+// keys in vt_key order within 16-key groups.  One workgroup per 32 keys of
+// one KV head, through LDS.
+__global__ void __launch_bounds__(256)
+v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt, int T, int D,
+                   int Tp) {
+    __shared__ __align__(16) uint16_t tile[kAttnTile * (128 + 8)];
+    const int DS = D + 8;
+    const int nkb = Tp / kAttnTile;
+    const int g = blockIdx.x / nkb, kb = blockIdx.x % nkb;
+    const uint16_t* vg = v + (int64_t)g * T * D;
+    const int dc = D / 8;
+    for (int c = threadIdx.x; c < kAttnTile * dc; c += blockDim.x) {
+        const int key = c / dc, d = 8 * (c % dc);
+        const int j = kb * kAttnTile + key;
+        h8 x = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (j < T) x = ld_h8(vg + (int64_t)j * D + d);
+        *reinterpret_cast<h8*>(&tile[key * DS + d]) = x;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < D * 4; c += blockDim.x) {
+        const int d = c >> 2, pg = c & 3;   // positions 8 pg .. 8 pg + 7 of the 32
+        uint16_t o[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int p = 8 * pg + t;
+            o[t] = tile[(16 * (p >> 4) + vt_key(p & 15)) * DS + d];
+        }
+        uint4 w;
+        w.x = o[0] | ((uint32_t)o[1] << 16);
+        w.y = o[2] | ((uint32_t)o[3] << 16);
+        w.z = o[4] | ((uint32_t)o[5] << 16);
+        w.w = o[6] | ((uint32_t)o[7] << 16);
+        *reinterpret_cast<uint4*>(vt + ((int64_t)g * D + d) * Tp + kb * kAttnTile + 8 * pg) = w;
+    }
+}
+
 // One workgroup: KV head `g`, query heads g * gs + chunk * 4 + wave, queries
-// q0 .. q0 + 31.  DP = head dim rounded up to 32 (D % 8 == 0, D <= DP).
+// q0 .. q0 + 31.  DP = head dim rounded up to 32 (D % 8 == 0, D <= DP).  K
+// and V^T blocks are double-buffered in LDS: the block after next is in
+// flight in registers while the current one is multiplied, one barrier per
+// block.
 template <int DP>
 __global__ void __launch_bounds__(kAttnWaves * 64, 2)
 attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                 const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
-                 int T, int D, float sm_scale, int window, int chunks, int n_qb) {
+                 const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int n_q, int n_kv,
+                 int T, int Tp, int D, float sm_scale, int window, int chunks, int n_qb) {
     constexpr int KS = DP + 8;            // K row stride in LDS (halves)
-    constexpr int VS = kAttnTile + 4;     // V^T row stride in LDS (halves)
-    constexpr int NC = 4 * DP;            // 16-byte chunks per 32-key block of K (and of V)
-    constexpr int PT = (NC + kAttnWaves * 64 - 1) / (kAttnWaves * 64);
+    constexpr int VS = kAttnTile + 8;     // V^T row stride in LDS (halves)
+    constexpr int NC = 4 * DP;            // 16-byte chunks per block of K (and of V^T)
+    constexpr int NT = kAttnWaves * 64;
+    constexpr int PT = (NC + NT - 1) / NT;
     constexpr int NKK = DP / 16;          // score MFMAs per block
     constexpr int NDB = DP / 32;          // d blocks of O^T
-    __shared__ __align__(16) uint16_t Ks[kAttnTile * KS];
-    __shared__ __align__(16) uint16_t Vt[DP * VS];
+    constexpr int DC = DP / 8;            // K chunks per key
+    __shared__ __align__(16) uint16_t Ks[2][kAttnTile * KS];
+    __shared__ __align__(16) uint16_t Vs[2][DP * VS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
@@ -76,7 +127,7 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const int qi = q0 + col;                         // this lane's query
 
     const uint16_t* Kg = k + (int64_t)g * T * D;
-    const uint16_t* Vg = v + (int64_t)g * T * D;
+    const uint16_t* Vg = vt + (int64_t)g * D * Tp;
 
     // Q tile (B operand of the score product), zero past D and past T.
     h8 qf[NKK];
@@ -93,32 +144,32 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const int lo = window > 0 ? max(0, q0 - window + 1) : 0;
     const int kb_lo = lo / kAttnTile, kb_hi = hi / kAttnTile;
     const int left = window > 0 ? qi - window + 1 : 0;   // this lane's first key
+    const float c1 = sm_scale * kLog2e;
 
-    // Block loads: chunk c -> key c % 32, d 8 (c / 32); lanes of a wave run
-    // over keys so the transposed V writes spread over LDS banks.
+    // Block loads are unconditional (no divergent branches around them): a
+    // K row past T is read from row T - 1 (its scores are always masked: key
+    // > every query), V^T is zero-padded to Tp keys, and a 16-byte chunk past
+    // D (DP > D) is read from the row start and replaced by zeros.
     h8 kr[PT], vr[PT];
     auto load_block = [&](int kb) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
-            const int c = tid + p * kAttnWaves * 64;
-            const int key = kb * kAttnTile + (c & 31), d = 8 * (c >> 5);
-            const bool ok = c < NC && key < T && d < D;
-            kr[p] = ok ? ld_h8(Kg + (int64_t)key * D + d) : h8{0, 0, 0, 0, 0, 0, 0, 0};
-            vr[p] = ok ? ld_h8(Vg + (int64_t)key * D + d) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            const int c = min(tid + p * NT, NC - 1);
+            const int key = min(kb * kAttnTile + c / DC, T - 1), kd = 8 * (c % DC);
+            const h8 x = ld_h8(Kg + (int64_t)key * D + (kd < D ? kd : 0));
+            kr[p] = kd < D ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            const int vd = c >> 2, vp = 8 * (c & 3);
+            const h8 y = ld_h8(Vg + (int64_t)(vd < D ? vd : 0) * Tp + kb * kAttnTile + vp);
+            vr[p] = vd < D ? y : h8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     };
-    auto store_block = [&]() {
+    auto store_block = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
-            const int c = tid + p * kAttnWaves * 64;
+            const int c = tid + p * NT;
             if (c < NC) {
-                const int key = c & 31, d = 8 * (c >> 5);
-                *reinterpret_cast<h8*>(&Ks[key * KS + d]) = kr[p];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    _Float16 x = vr[p][e];
-                    Vt[(d + e) * VS + key] = __builtin_bit_cast(uint16_t, x);
-                }
+                *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) = kr[p];
+                *reinterpret_cast<h8*>(&Vs[buf][(c >> 2) * VS + 8 * (c & 3)]) = vr[p];
             }
         }
     };
@@ -128,68 +179,90 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc_o[db][i] = 0.0f;
+    // m_run: running maximum in units of score * sm_scale * log2(e); the
+    // accumulators are rescaled only when a new maximum exceeds it by more
+    // than 8 (probabilities relative to m_run then stay <= 2^8).
     float m_run = kMasked, l_run = 0.0f;
 
-    load_block(kb_lo);
-    for (int kb = kb_lo; kb <= kb_hi; ++kb) {
-        __syncthreads();                 // previous block's LDS reads are done
-        store_block();
-        __syncthreads();
-        if (kb < kb_hi) load_block(kb + 1);
-        if (!active) continue;
-
+    // One 32-key block: scores, online softmax, V product.  `full`: every
+    // key of the block is visible to all 32 queries of the tile (no mask).
+    auto block = [&](int kb, int buf, bool full) {
         // S^T = K Q^T
         f16x s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-            const h8 a = *reinterpret_cast<const h8*>(&Ks[col * KS + 16 * kk + 8 * hh]);
+            const h8 a = *reinterpret_cast<const h8*>(&Ks[buf][col * KS + 16 * kk + 8 * hh]);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s, 0, 0, 0);
         }
-
-        // mask, scale (score rounded to fp16 first), running max
-        const int kbase = kb * kAttnTile + 4 * hh;
-        float mloc = kMasked;
-        bool ok[16];
+        __builtin_amdgcn_sched_barrier(0);
+        // scores rounded to fp16 (the reference stores S in fp16); masked
+        // scores become -inf (weight exp2(-inf) = 0); the max is taken before
+        // scaling (sm_scale > 0 keeps the order)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int j = kbase + 8 * (i >> 2) + (i & 3);
-            ok[i] = j <= qi && j >= left;
-            const float x = h2f(f2h(s[i])) * sm_scale;
-            s[i] = x;
-            mloc = ok[i] ? fmaxf(mloc, x) : mloc;
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = exp2f((m_run - m_new) * kLog2e);
-        m_run = m_new;
-
-        h8 pb[2];
-        float lsum = 0.0f;
+        for (int i = 0; i < 16; ++i) s[i] = (float)(_Float16)s[i];
+        if (!full) {
+            const int kbase = kb * kAttnTile + 4 * hh;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float e = ok[i] ? exp2f((s[i] - m_new) * kLog2e) : 0.0f;
-            const _Float16 e16 = (_Float16)e;
-            lsum += (float)e16;
-            pb[i >> 3][i & 7] = e16;
-        }
-        l_run = l_run * alpha + lsum;
-
-        // O^T = alpha O^T + V^T P^T
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc_o[db][i] *= alpha;
-            const uint16_t* vrow = &Vt[(32 * db + col) * VS + 4 * hh];
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const h4 a0 = *reinterpret_cast<const h4*>(vrow + 16 * k2);
-                const h4 a1 = *reinterpret_cast<const h4*>(vrow + 16 * k2 + 8);
-                const h8 a = h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-                acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[k2], acc_o[db], 0, 0, 0);
+            for (int i = 0; i < 16; ++i) {
+                const int j = kbase + 8 * (i >> 2) + (i & 3);
+                s[i] = (j <= qi && j >= left) ? s[i] : -__builtin_inff();
             }
         }
+        float mloc = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * c1;
+        const bool grow = mloc > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - mloc) : 1.0f;
+            m_run = grow ? mloc : m_run;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc_o[db][i] *= alpha;
+        }
+        h8 pb[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            pb[i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c1, -m_run));
+        // l_run sums the fp16 weights the V product uses (v_dot2: exact pairs)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            l_run = __builtin_amdgcn_fdot2(
+                h2{pb[i >> 2][2 * (i & 3)], pb[i >> 2][2 * (i & 3) + 1]}, h2{1, 1}, l_run, false);
+        __builtin_amdgcn_sched_barrier(0);
+        // O^T += V^T P^T
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const h8 a =
+                    *reinterpret_cast<const h8*>(&Vs[buf][(32 * db + col) * VS + 16 * k2 + 8 * hh]);
+                acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[k2], acc_o[db], 0, 0, 0);
+            }
+    };
+
+    const int nkb = kb_hi - kb_lo + 1;
+    load_block(kb_lo);
+    store_block(0);
+    __syncthreads();
+    if (nkb > 1) load_block(kb_lo + 1);
+    for (int it = 0; it < nkb; ++it) {
+        const int kb = kb_lo + it, buf = it & 1;
+        if (it + 1 < nkb) {
+            store_block(buf ^ 1);
+            if (it + 2 < nkb) load_block(kb + 2);
+        }
+        if (active) {
+            // every key of the block visible to all 32 queries of the tile
+            const bool full = kb * kAttnTile + kAttnTile - 1 <= q0 &&
+                              (window <= 0 || kb * kAttnTile >= q0 + kAttnTile - window);
+            block(kb, buf, full);
+        }
+        __syncthreads();
     }
 
     if (!active || qi >= T) return;
@@ -267,25 +340,32 @@ inline unsigned blocks_for(int64_t n, int threads) {
 
 int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
 
+size_t attention_workspace_bytes(int n_kv, int T, int D) {
+    const int64_t Tp = ((int64_t)T + kAttnTile - 1) / kAttnTile * kAttnTile;
+    return (size_t)n_kv * (size_t)D * (size_t)Tp * 2;
+}
+
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                    uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
-                                    int window, hipStream_t stream) {
+                                    uint16_t* out, uint16_t* vt_ws, int n_q, int n_kv, int T,
+                                    int D, float sm_scale, int window, hipStream_t stream) {
     const int gs = n_q / n_kv;
     const int chunks = (gs + kAttnWaves - 1) / kAttnWaves;
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;
+    const int Tp = n_qb * kAttnTile;
+    v_transpose_kernel<<<n_kv * n_qb, 256, 0, stream>>>(v, vt_ws, T, D, Tp);
     const dim3 grid((unsigned)(n_qb * n_kv * chunks)), block(kAttnWaves * 64);
     switch (attention_padded_dim(D)) {
         case 32:
-            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                             sm_scale, window, chunks, n_qb);
+            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
+                                                             D, sm_scale, window, chunks, n_qb);
             break;
         case 64:
-            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                             sm_scale, window, chunks, n_qb);
+            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
+                                                             D, sm_scale, window, chunks, n_qb);
             break;
         case 128:
-            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                              sm_scale, window, chunks, n_qb);
+            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
+                                                              D, sm_scale, window, chunks, n_qb);
             break;
         default:
             return hipErrorInvalidValue;
