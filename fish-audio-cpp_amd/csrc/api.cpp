@@ -56,8 +56,6 @@ struct Workspace {
     size_t st_bytes = 0;
     uint16_t* yt = nullptr;     // fp16 [N, 2F] of the SwiGLU entry's separate-launch path
     size_t yt_bytes = 0;
-    uint16_t* vt = nullptr;     // transposed V of prefill attention (NULL workspace)
-    size_t vt_bytes = 0;
 };
 
 thread_local std::unordered_map<int, Workspace> g_ws;
@@ -548,15 +546,11 @@ int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int
     return FA_OK;
 }
 
-size_t fa_prefill_attention_workspace_bytes(int n_kv, int T, int D) {
-    if (n_kv <= 0 || T < 0 || D <= 0) return 0;
-    return fa::attention_workspace_bytes(n_kv, T, D);
-}
-
 int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                          void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
                          void* stream, int window_size) {
     const char* fn = "fa_prefill_attention";
+    (void)workspace;   // the fused kernel keeps scores on chip and needs no scratch
     g_err.clear();
     if (T < 0 || n_q <= 0 || n_kv <= 0 || D <= 0)
         return fail(FA_ERR_INVALID_ARG, "%s: bad n_q=%d n_kv=%d T=%d D=%d", fn, n_q, n_kv, T, D);
@@ -571,24 +565,10 @@ int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
         return fail(FA_ERR_INVALID_ARG, "%s: q larger than 2^31 elements", fn);
     if (T == 0) return FA_OK;
     if (!q || !k || !v || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
-        (workspace && !aligned16(workspace)))
-        return fail(FA_ERR_INVALID_ARG,
-                    "%s: q, k, v, out and workspace must be 16-byte aligned", fn);
-    hipStream_t s = (hipStream_t)stream;
-    uint16_t* vt = (uint16_t*)workspace;
-    if (!vt) {
-        Workspace* ws = nullptr;
-        int rc = current_ws(&ws);
-        if (rc) return rc;
-        void* p = ws->vt;
-        rc = grow(&p, &ws->vt_bytes, fa::attention_workspace_bytes(n_kv, T, D), s);
-        ws->vt = (uint16_t*)p;
-        if (rc) return rc;
-        vt = ws->vt;
-    }
-    FA_HIP(fa::launch_prefill_attention(q, k, v, out, vt, n_q, n_kv, T, D, sm_scale, window_size,
-                                        s));
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 16-byte aligned", fn);
+    FA_HIP(fa::launch_prefill_attention(q, k, v, out, n_q, n_kv, T, D, sm_scale, window_size,
+                                        (hipStream_t)stream));
     return FA_OK;
 }
 

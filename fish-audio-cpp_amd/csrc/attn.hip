@@ -47,66 +47,33 @@ __device__ __forceinline__ h8 ld_h8(const uint16_t* p) {
     return *reinterpret_cast<const h8*>(p);
 }
 
-// V^T key order: within each 16-key group, position p = 8h + t holds key
-// 4h + t (t < 4) or 8 + 4h + (t - 4) (t >= 4) -- the k-slot order of the P^T
-// operand -- so one 16-byte LDS read gives a lane its 8 V^T slots.
-__device__ __forceinline__ int vt_key(int p) {   // key offset (0..15) at position p
-    const int h = p >> 3, t = p & 7;
-    return t < 4 ? 4 * h + t : 8 + 4 * h + (t - 4);
-}
-
-// v [n_kv, T, D] -> vt [n_kv, D, Tp] (Tp = T rounded up to 32, zero past T),
-// keys in vt_key order within 16-key groups.  One workgroup per 32 keys of
-// one KV head, through LDS.
-__global__ void __launch_bounds__(256)
-v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt, int T, int D,
-                   int Tp) {
-    __shared__ __align__(16) uint16_t tile[kAttnTile * (128 + 8)];
-    const int DS = D + 8;
-    const int nkb = Tp / kAttnTile;
-    const int g = blockIdx.x / nkb, kb = blockIdx.x % nkb;
-    const uint16_t* vg = v + (int64_t)g * T * D;
-    const int dc = D / 8;
-    for (int c = threadIdx.x; c < kAttnTile * dc; c += blockDim.x) {
-        const int key = c / dc, d = 8 * (c % dc);
-        const int j = kb * kAttnTile + key;
-        h8 x = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (j < T) x = ld_h8(vg + (int64_t)j * D + d);
-        *reinterpret_cast<h8*>(&tile[key * DS + d]) = x;
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < D * 4; c += blockDim.x) {
-        const int d = c >> 2, pg = c & 3;   // positions 8 pg .. 8 pg + 7 of the 32
-        uint16_t o[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int p = 8 * pg + t;
-            o[t] = tile[(16 * (p >> 4) + vt_key(p & 15)) * DS + d];
-        }
-        uint4 w;
-        w.x = o[0] | ((uint32_t)o[1] << 16);
-        w.y = o[2] | ((uint32_t)o[3] << 16);
-        w.z = o[4] | ((uint32_t)o[5] << 16);
-        w.w = o[6] | ((uint32_t)o[7] << 16);
-        *reinterpret_cast<uint4*>(vt + ((int64_t)g * D + d) * Tp + kb * kAttnTile + 8 * pg) = w;
-    }
+// Position of key offset o (0..31) in a V^T row of LDS: within each 16-key
+// group, position 8h + t holds key 4h + t (t < 4) or 8 + 4h + (t - 4)
+// (t >= 4) -- the k-slot order of the P^T operand -- so one 16-byte LDS read
+// gives a lane its 8 V^T slots.  Keys 2m and 2m + 1 land on adjacent
+// positions.
+__device__ __forceinline__ int vt_pos(int o) {
+    return 16 * (o >> 4) + 8 * ((o & 7) >> 2) + 4 * ((o >> 3) & 1) + (o & 3);
 }
 
 // One workgroup: KV head `g`, query heads g * gs + chunk * 4 + wave, queries
 // q0 .. q0 + 31.  DP = head dim rounded up to 32 (D % 8 == 0, D <= DP).  K
 // and V^T blocks are double-buffered in LDS: the block after next is in
 // flight in registers while the current one is multiplied, one barrier per
-// block.
+// block.  V is transposed on its way into LDS: a thread loads the same 8 d of
+// two adjacent keys and writes 8 packed key pairs.
 template <int DP>
 __global__ void __launch_bounds__(kAttnWaves * 64, 2)
 attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                 const uint16_t* __restrict__ vt, uint16_t* __restrict__ out, int n_q, int n_kv,
-                 int T, int Tp, int D, float sm_scale, int window, int chunks, int n_qb) {
+                 const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
+                 int T, int D, float sm_scale, int window, int chunks, int n_qb) {
     constexpr int KS = DP + 8;            // K row stride in LDS (halves)
     constexpr int VS = kAttnTile + 8;     // V^T row stride in LDS (halves)
-    constexpr int NC = 4 * DP;            // 16-byte chunks per block of K (and of V^T)
+    constexpr int NC = 4 * DP;            // 16-byte chunks per block of K
     constexpr int NT = kAttnWaves * 64;
     constexpr int PT = (NC + NT - 1) / NT;
+    constexpr int NU = 2 * DP;            // V units per block: key pair x 8 d
+    constexpr int PV = (NU + NT - 1) / NT;
     constexpr int NKK = DP / 16;          // score MFMAs per block
     constexpr int NDB = DP / 32;          // d blocks of O^T
     constexpr int DC = DP / 8;            // K chunks per key
@@ -127,7 +94,7 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const int qi = q0 + col;                         // this lane's query
 
     const uint16_t* Kg = k + (int64_t)g * T * D;
-    const uint16_t* Vg = vt + (int64_t)g * D * Tp;
+    const uint16_t* Vg = v + (int64_t)g * T * D;
 
     // Q tile (B operand of the score product), zero past D and past T.
     h8 qf[NKK];
@@ -147,10 +114,10 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float c1 = sm_scale * kLog2e;
 
     // Block loads are unconditional (no divergent branches around them): a
-    // K row past T is read from row T - 1 (its scores are always masked: key
-    // > every query), V^T is zero-padded to Tp keys, and a 16-byte chunk past
-    // D (DP > D) is read from the row start and replaced by zeros.
-    h8 kr[PT], vr[PT];
+    // row past T is read from row T - 1 (its scores are always masked: key
+    // > every query, so its weight is exactly 0), and a 16-byte chunk past D
+    // (DP > D) is read from the row start and replaced by zeros.
+    h8 kr[PT], vr[PV][2];
     auto load_block = [&](int kb) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
@@ -158,18 +125,34 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
             const int key = min(kb * kAttnTile + c / DC, T - 1), kd = 8 * (c % DC);
             const h8 x = ld_h8(Kg + (int64_t)key * D + (kd < D ? kd : 0));
             kr[p] = kd < D ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
-            const int vd = c >> 2, vp = 8 * (c & 3);
-            const h8 y = ld_h8(Vg + (int64_t)(vd < D ? vd : 0) * Tp + kb * kAttnTile + vp);
-            vr[p] = vd < D ? y : h8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int p = 0; p < PV; ++p) {
+            const int u = min(tid + p * NT, NU - 1);
+            const int key = kb * kAttnTile + 2 * (u & 15), vd = 8 * (u >> 4);
+            const int off = vd < D ? vd : 0;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const h8 y = ld_h8(Vg + (int64_t)min(key + r, T - 1) * D + off);
+                vr[p][r] = vd < D ? y : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
         }
     };
     auto store_block = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
             const int c = tid + p * NT;
-            if (c < NC) {
-                *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) = kr[p];
-                *reinterpret_cast<h8*>(&Vs[buf][(c >> 2) * VS + 8 * (c & 3)]) = vr[p];
+            if (c < NC) *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) = kr[p];
+        }
+#pragma unroll
+        for (int p = 0; p < PV; ++p) {
+            const int u = tid + p * NT;
+            if (u < NU) {
+                const int pos = vt_pos(2 * (u & 15)), vd = 8 * (u >> 4);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    *reinterpret_cast<h2*>(&Vs[buf][(vd + e) * VS + pos]) =
+                        h2{vr[p][0][e], vr[p][1][e]};
             }
         }
     };
@@ -340,32 +323,25 @@ inline unsigned blocks_for(int64_t n, int threads) {
 
 int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
 
-size_t attention_workspace_bytes(int n_kv, int T, int D) {
-    const int64_t Tp = ((int64_t)T + kAttnTile - 1) / kAttnTile * kAttnTile;
-    return (size_t)n_kv * (size_t)D * (size_t)Tp * 2;
-}
-
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                    uint16_t* out, uint16_t* vt_ws, int n_q, int n_kv, int T,
-                                    int D, float sm_scale, int window, hipStream_t stream) {
+                                    uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                    int window, hipStream_t stream) {
     const int gs = n_q / n_kv;
     const int chunks = (gs + kAttnWaves - 1) / kAttnWaves;
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;
-    const int Tp = n_qb * kAttnTile;
-    v_transpose_kernel<<<n_kv * n_qb, 256, 0, stream>>>(v, vt_ws, T, D, Tp);
     const dim3 grid((unsigned)(n_qb * n_kv * chunks)), block(kAttnWaves * 64);
     switch (attention_padded_dim(D)) {
         case 32:
-            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
-                                                             D, sm_scale, window, chunks, n_qb);
+            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                             sm_scale, window, chunks, n_qb);
             break;
         case 64:
-            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
-                                                             D, sm_scale, window, chunks, n_qb);
+            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                             sm_scale, window, chunks, n_qb);
             break;
         case 128:
-            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, vt_ws, out, n_q, n_kv, T, Tp,
-                                                              D, sm_scale, window, chunks, n_qb);
+            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
+                                                              sm_scale, window, chunks, n_qb);
             break;
         default:
             return hipErrorInvalidValue;

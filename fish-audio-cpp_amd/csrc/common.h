@@ -206,14 +206,10 @@ hipError_t launch_gemm_f16_generic(const uint16_t* W, const uint16_t* X, uint16_
 
 // Prefill attention side (attn.hip).  attention_padded_dim gives the head dim
 // the fused attention kernel is instantiated for (32, 64 or 128), 0 if D > 128.
-// The kernel reads V transposed ([n_kv, D, T rounded up to 32], keys in the
-// score operand's slot order) from `vt_ws`, attention_workspace_bytes long,
-// written by a first launch.
 int attention_padded_dim(int D);
-size_t attention_workspace_bytes(int n_kv, int T, int D);
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                    uint16_t* out, uint16_t* vt_ws, int n_q, int n_kv, int T,
-                                    int D, float sm_scale, int window, hipStream_t stream);
+                                    uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                    int window, hipStream_t stream);
 hipError_t launch_qkv_split(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
                             int n_q, int n_kv, int D, bool vec, hipStream_t stream);
 hipError_t launch_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D, bool vec,

@@ -86,7 +86,6 @@ SIGNATURES = {
     "fa_qkv_split_heads_gqa": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "fa_qkv_split_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_merge_heads": (_i, [_p, _p, _i, _i, _i, _p]),
-    "fa_prefill_attention_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i]),
     "fa_prefill_attention": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i]),
     "fa_workspace_reserve": (_i, [_i, _i, _i, _i, _p]),
     "fa_workspace_release": (_i, []),

@@ -19,7 +19,6 @@
 #ifndef FISH_W8A8_H
 #define FISH_W8A8_H
 
-#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -203,15 +202,11 @@ int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int
  * KV head h / (n_q / n_kv); window_size > 0 limits query i to keys
  * i - window_size + 1 .. i.  q / out [n_q, T, D], k / v [n_kv, T, D], fp16,
  * head-major, 16-byte aligned; D % 8 == 0 and D <= 128; n_q % n_kv == 0;
- * sm_scale > 0.  The T x T scores stay on chip (one fused kernel); the
- * workspace holds V transposed: fa_prefill_attention_workspace_bytes(n_kv, T, D)
- * bytes, 16-byte aligned (a buffer sized for the reference's kernel,
- * (n_q T T + 2 n_q T D) halves, is large enough when T >= 32), or NULL for the
- * library's per-thread scratch.  The reference's cuBLAS handle has no
- * counterpart.  Results agree with the reference within the order of fp32 sums
- * (scores are rounded to fp16 before scaling, probabilities enter the V
+ * sm_scale > 0.  One fused kernel: the T x T scores stay on chip, so
+ * `workspace` is not used (it may be NULL; the reference's cuBLAS handle has no
+ * counterpart).  Results agree with the reference within the order of fp32
+ * sums (scores are rounded to fp16 before scaling, probabilities enter the V
  * product as fp16). */
-size_t fa_prefill_attention_workspace_bytes(int n_kv, int T, int D);
 int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                          void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
                          void* stream, int window_size);
