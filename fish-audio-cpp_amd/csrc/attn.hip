@@ -113,18 +113,18 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const int left = window > 0 ? qi - window + 1 : 0;   // this lane's first key
     const float c1 = sm_scale * kLog2e;
 
-    // Block loads are unconditional (no divergent branches around them): a
-    // row past T is read from row T - 1 (its scores are always masked: key
-    // > every query, so its weight is exactly 0), and a 16-byte chunk past D
-    // (DP > D) is read from the row start and replaced by zeros.
+    // Block loads are unconditional and their values are not touched until
+    // the store one iteration later (so no wait follows the issue): a row
+    // past T is read from row T - 1 (its scores are always masked: key >
+    // every query, so its weight is exactly 0), and a 16-byte chunk past D
+    // (DP > D) is read from the row start and zeroed at the store.
     h8 kr[PT], vr[PV][2];
     auto load_block = [&](int kb) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
             const int c = min(tid + p * NT, NC - 1);
             const int key = min(kb * kAttnTile + c / DC, T - 1), kd = 8 * (c % DC);
-            const h8 x = ld_h8(Kg + (int64_t)key * D + (kd < D ? kd : 0));
-            kr[p] = kd < D ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
+            kr[p] = ld_h8(Kg + (int64_t)key * D + (kd < D ? kd : 0));
         }
 #pragma unroll
         for (int p = 0; p < PV; ++p) {
@@ -132,27 +132,29 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
             const int key = kb * kAttnTile + 2 * (u & 15), vd = 8 * (u >> 4);
             const int off = vd < D ? vd : 0;
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const h8 y = ld_h8(Vg + (int64_t)min(key + r, T - 1) * D + off);
-                vr[p][r] = vd < D ? y : h8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
+            for (int r = 0; r < 2; ++r)
+                vr[p][r] = ld_h8(Vg + (int64_t)min(key + r, T - 1) * D + off);
         }
     };
+    const h8 z8 = h8{0, 0, 0, 0, 0, 0, 0, 0};
     auto store_block = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < PT; ++p) {
             const int c = tid + p * NT;
-            if (c < NC) *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) = kr[p];
+            if (c < NC)
+                *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) =
+                    (DP == 128 || 8 * (c % DC) < D) ? kr[p] : z8;
         }
 #pragma unroll
         for (int p = 0; p < PV; ++p) {
             const int u = tid + p * NT;
             if (u < NU) {
                 const int pos = vt_pos(2 * (u & 15)), vd = 8 * (u >> 4);
+                const bool in = DP == 128 || vd < D;
+                const h8 v0 = in ? vr[p][0] : z8, v1 = in ? vr[p][1] : z8;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    *reinterpret_cast<h2*>(&Vs[buf][(vd + e) * VS + pos]) =
-                        h2{vr[p][0][e], vr[p][1][e]};
+                    *reinterpret_cast<h2*>(&Vs[buf][(vd + e) * VS + pos]) = h2{v0[e], v1[e]};
             }
         }
     };
