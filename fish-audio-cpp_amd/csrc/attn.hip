@@ -56,31 +56,44 @@ __device__ __forceinline__ int vt_pos(int o) {
     return 16 * (o >> 4) + 8 * ((o & 7) >> 2) + 4 * ((o >> 3) & 1) + (o & 3);
 }
 
-// One workgroup: KV head `g`, query heads g * gs + chunk * 4 + wave, queries
-// q0 .. q0 + 31.  DP = head dim rounded up to 32 (D % 8 == 0, D <= DP).  K
-// and V^T blocks are double-buffered in LDS: the block after next is in
-// flight in registers while the current one is multiplied, one barrier per
-// block.  V is transposed on its way into LDS: a thread loads the same 8 d of
-// two adjacent keys and writes 8 packed key pairs.
+// One workgroup: KV head `g`, query heads g * gs + chunk * 4 + (wave & 3),
+// queries q0 .. q0 + 31; DP = head dim rounded up to 32 (D % 8 == 0,
+// D <= DP).  The tile's key blocks are split in two halves: waves 0-3 take the
+// first, waves 4-7 the second (each half with its own double-buffered K / V^T
+// blocks in LDS and its own online softmax), and the halves are merged
+// through LDS at the end.  Splitting the key range halves the serial chain of
+// the tiles next to the diagonal of long sequences, which would otherwise
+// set the kernel's duration.  Within a half, the block after next is in
+// flight in registers while the current one is multiplied (one barrier per
+// block), and V is transposed on its way into LDS: a thread loads the same
+// 8 d of two adjacent keys and writes 8 packed key pairs.
 template <int DP>
-__global__ void __launch_bounds__(kAttnWaves * 64, 2)
+constexpr int attn_lds_bytes() {
+    return 2 * 2 * (kAttnTile * (DP + 8) + DP * (kAttnTile + 8)) * 2;
+}
+
+template <int DP>
+__global__ void __launch_bounds__(2 * kAttnWaves * 64, 1)
 attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                  const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
                  int T, int D, float sm_scale, int window, int chunks, int n_qb) {
     constexpr int KS = DP + 8;            // K row stride in LDS (halves)
     constexpr int VS = kAttnTile + 8;     // V^T row stride in LDS (halves)
     constexpr int NC = 4 * DP;            // 16-byte chunks per block of K
-    constexpr int NT = kAttnWaves * 64;
+    constexpr int NT = kAttnWaves * 64;   // threads per half
     constexpr int PT = (NC + NT - 1) / NT;
     constexpr int NU = 2 * DP;            // V units per block: key pair x 8 d
     constexpr int PV = (NU + NT - 1) / NT;
     constexpr int NKK = DP / 16;          // score MFMAs per block
     constexpr int NDB = DP / 32;          // d blocks of O^T
     constexpr int DC = DP / 8;            // K chunks per key
-    __shared__ __align__(16) uint16_t Ks[2][kAttnTile * KS];
-    __shared__ __align__(16) uint16_t Vs[2][DP * VS];
+    constexpr int KB = kAttnTile * KS, VB = DP * VS;   // halves per K / V^T buffer
+    extern __shared__ __align__(16) uint16_t lds[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = threadIdx.x / NT;
+    const int tid = threadIdx.x % NT, lane = tid & 63, wave = tid >> 6;
+    uint16_t* const Ks = lds + half * 2 * (KB + VB);   // [2][KB]
+    uint16_t* const Vs = Ks + 2 * KB;                 // [2][VB]
     const int col = lane & 31, hh = lane >> 5;
     const int gs = n_q / n_kv;
     // heaviest (last) query tiles first: they have the most key blocks
@@ -142,7 +155,7 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         for (int p = 0; p < PT; ++p) {
             const int c = tid + p * NT;
             if (c < NC)
-                *reinterpret_cast<h8*>(&Ks[buf][(c / DC) * KS + 8 * (c % DC)]) =
+                *reinterpret_cast<h8*>(&Ks[buf * KB + (c / DC) * KS + 8 * (c % DC)]) =
                     (DP == 128 || 8 * (c % DC) < D) ? kr[p] : z8;
         }
 #pragma unroll
@@ -154,7 +167,7 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                 const h8 v0 = in ? vr[p][0] : z8, v1 = in ? vr[p][1] : z8;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    *reinterpret_cast<h2*>(&Vs[buf][(vd + e) * VS + pos]) = h2{v0[e], v1[e]};
+                    *reinterpret_cast<h2*>(&Vs[buf * VB + (vd + e) * VS + pos]) = h2{v0[e], v1[e]};
             }
         }
     };
@@ -172,16 +185,26 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     // One 32-key block: scores, online softmax, V product.  `full`: every
     // key of the block is visible to all 32 queries of the tile (no mask).
     auto block = [&](int kb, int buf, bool full) {
+        // every operand read of the block is issued up front: one LDS round
+        // trip per block, the V^T reads complete under the softmax
+        h8 ka[NKK], va[NDB][2];
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            ka[kk] = *reinterpret_cast<const h8*>(&Ks[buf * KB + col * KS + 16 * kk + 8 * hh]);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+                va[db][k2] = *reinterpret_cast<const h8*>(
+                    &Vs[buf * VB + (32 * db + col) * VS + 16 * k2 + 8 * hh]);
+        __builtin_amdgcn_sched_barrier(0);
         // S^T = K Q^T
         f16x s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-            const h8 a = *reinterpret_cast<const h8*>(&Ks[buf][col * KS + 16 * kk + 8 * hh]);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s, 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int kk = 0; kk < NKK; ++kk)
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kk], qf[kk], s, 0, 0, 0);
         // scores rounded to fp16 (the reference stores S in fp16); masked
         // scores become -inf (weight exp2(-inf) = 0); the max is taken before
         // scaling (sm_scale > 0 keeps the order)
@@ -218,30 +241,32 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         for (int i = 0; i < 8; ++i)
             l_run = __builtin_amdgcn_fdot2(
                 h2{pb[i >> 2][2 * (i & 3)], pb[i >> 2][2 * (i & 3) + 1]}, h2{1, 1}, l_run, false);
-        __builtin_amdgcn_sched_barrier(0);
         // O^T += V^T P^T
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const h8 a =
-                    *reinterpret_cast<const h8*>(&Vs[buf][(32 * db + col) * VS + 16 * k2 + 8 * hh]);
-                acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[k2], acc_o[db], 0, 0, 0);
-            }
+            for (int k2 = 0; k2 < 2; ++k2)
+                acc_o[db] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][k2], pb[k2], acc_o[db], 0, 0, 0);
     };
 
-    const int nkb = kb_hi - kb_lo + 1;
-    load_block(kb_lo);
-    store_block(0);
+    // this half's key blocks: the first ceil(n / 2) of the tile's n blocks,
+    // or the rest
+    const int nkb = kb_hi - kb_lo + 1, n0 = (nkb + 1) / 2;
+    const int my_lo = half ? kb_lo + n0 : kb_lo, my_n = half ? nkb - n0 : n0;
+    if (my_n > 0) {
+        load_block(my_lo);
+        store_block(0);
+    }
     __syncthreads();
-    if (nkb > 1) load_block(kb_lo + 1);
-    for (int it = 0; it < nkb; ++it) {
-        const int kb = kb_lo + it, buf = it & 1;
-        if (it + 1 < nkb) {
+    if (my_n > 1) load_block(my_lo + 1);
+    for (int it = 0; it < n0; ++it) {
+        const int kb = my_lo + it, buf = it & 1;
+        if (it + 1 < my_n) {
             store_block(buf ^ 1);
-            if (it + 2 < nkb) load_block(kb + 2);
+            if (it + 2 < my_n) load_block(kb + 2);
         }
-        if (active) {
+        if (active && it < my_n) {
             // every key of the block visible to all 32 queries of the tile
             const bool full = kb * kAttnTile + kAttnTile - 1 <= q0 &&
                               (window <= 0 || kb * kAttnTile >= q0 + kAttnTile - window);
@@ -250,8 +275,25 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         __syncthreads();
     }
 
-    if (!active || qi >= T) return;
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    // merge: the second half's waves leave (m, l, O^T) in LDS, lane-major
+    // ([wave][value][lane] floats: conflict-free), the first half's combine
+    // them with their own and write the output.
+    constexpr int NV = 16 * NDB + 2;
+    float* const red = reinterpret_cast<float*>(lds) + wave * NV * 64 + lane;
+    if (half == 1 && active) {
+        red[0] = m_run;
+        red[64] = l_run;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[(2 + 16 * db + i) * 64] = acc_o[db][i];
+    }
+    __syncthreads();
+    if (half == 1 || !active || qi >= T) return;
+    const float m1 = red[0], m = fmaxf(m_run, m1);
+    const float f0 = __builtin_amdgcn_exp2f(m_run - m), f1 = __builtin_amdgcn_exp2f(m1 - m);
+    const float l_lane = l_run * f0 + red[64] * f1;
+    const float l_tot = l_lane + __shfl_xor(l_lane, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t* orow = out + ((int64_t)head * T + qi) * D;
 #pragma unroll
@@ -262,7 +304,11 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
             if (d < D) {
                 uint16_t o4[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) o4[t] = f2h(acc_o[db][4 * r + t] * inv);
+                for (int t = 0; t < 4; ++t) {
+                    const int i = 4 * r + t;
+                    const float o = acc_o[db][i] * f0 + red[(2 + 16 * db + i) * 64] * f1;
+                    o4[t] = f2h(o * inv);
+                }
                 uint2 w;
                 w.x = (uint32_t)o4[0] | ((uint32_t)o4[1] << 16);
                 w.y = (uint32_t)o4[2] | ((uint32_t)o4[3] << 16);
@@ -321,6 +367,21 @@ inline unsigned blocks_for(int64_t n, int threads) {
     return (unsigned)((n + threads - 1) / threads);
 }
 
+template <int DP>
+hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                            uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                            int window, int chunks, int n_qb, hipStream_t stream) {
+    constexpr int lds = attn_lds_bytes<DP>();
+    static_assert(lds >= 4 * 64 * (DP / 2 + 2) * 4, "merge area exceeds the block buffers");
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&attention_kernel<DP>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    attention_kernel<DP><<<grid, 2 * kAttnWaves * 64, lds, stream>>>(
+        q, k, v, out, n_q, n_kv, T, D, sm_scale, window, chunks, n_qb);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
@@ -331,24 +392,20 @@ hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const 
     const int gs = n_q / n_kv;
     const int chunks = (gs + kAttnWaves - 1) / kAttnWaves;
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;
-    const dim3 grid((unsigned)(n_qb * n_kv * chunks)), block(kAttnWaves * 64);
+    const dim3 grid((unsigned)(n_qb * n_kv * chunks));
     switch (attention_padded_dim(D)) {
         case 32:
-            attention_kernel<32><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                             sm_scale, window, chunks, n_qb);
-            break;
+            return launch_attention<32>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
+                                        chunks, n_qb, stream);
         case 64:
-            attention_kernel<64><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                             sm_scale, window, chunks, n_qb);
-            break;
+            return launch_attention<64>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
+                                        chunks, n_qb, stream);
         case 128:
-            attention_kernel<128><<<grid, block, 0, stream>>>(q, k, v, out, n_q, n_kv, T, D,
-                                                              sm_scale, window, chunks, n_qb);
-            break;
+            return launch_attention<128>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
+                                         chunks, n_qb, stream);
         default:
             return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_qkv_split(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
