@@ -89,4 +89,27 @@ void int8_silu_mul_gemm_fp16(const int8_t* W, const __half* scale, int group_siz
                                 u16(gate), u16(up), u16(Y), M, N, K, stream));
 }
 
+void prefill_attention_gpu(const __half* q, const __half* k, const __half* v, __half* out,
+                           __half* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
+                           void* /*blas_handle_unused*/, hipStream_t stream, int window_size) {
+    check(fa_prefill_attention(u16(q), u16(k), u16(v), u16(out), workspace, n_q, n_kv, T, D,
+                               sm_scale, stream, window_size));
+}
+
+void qkv_split_heads(const __half* qkv, __half* q, __half* k, __half* v, int T, int n_heads,
+                     int head_dim, hipStream_t stream) {
+    check(fa_qkv_split_heads(u16(qkv), u16(q), u16(k), u16(v), T, n_heads, head_dim, stream));
+}
+
+void qkv_split_heads_gqa(const __half* qkv, __half* q, __half* k, __half* v, int T, int n_q,
+                         int n_kv, int head_dim, hipStream_t stream) {
+    check(fa_qkv_split_heads_gqa(u16(qkv), u16(q), u16(k), u16(v), T, n_q, n_kv, head_dim,
+                                 stream));
+}
+
+void merge_heads(const __half* heads, __half* out, int T, int n_heads, int head_dim,
+                 hipStream_t stream) {
+    check(fa_merge_heads(u16(heads), u16(out), T, n_heads, head_dim, stream));
+}
+
 }  // namespace fish::kernels

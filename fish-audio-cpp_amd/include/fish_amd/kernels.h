@@ -1,5 +1,5 @@
 // kernels.h -- C++ mirror of the reference's kernel API for the W8A8 path
-// (src/kernels/kernels.h:11-19, 111-140, 242-259), on HIP.
+// (src/kernels/kernels.h:11-19, 111-140, 242-259, 324-344), on HIP.
 //
 // Same names, argument order and meaning; hipStream_t replaces cudaStream_t,
 // and the cublasHandle_t slot of int8_dequant_gemm_fp16 becomes an unused
@@ -26,6 +26,20 @@ void int8_dequant_gemm_fp16(const int8_t* W, const __half* scale, int group_size
                             const __half* act_scale, const __half* smooth_inv, const __half* X,
                             __half* Y, int M, int N, int K, void* blas_handle_unused,
                             hipStream_t stream = 0);
+
+// Prefill attention side (src/kernels/kernels.h:324-344): the same names and
+// argument order; the cublasHandle_t of prefill_attention_gpu becomes an
+// unused opaque pointer and `workspace` may be null (the fused kernel needs
+// none).
+void prefill_attention_gpu(const __half* q, const __half* k, const __half* v, __half* out,
+                           __half* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
+                           void* blas_handle_unused, hipStream_t stream, int window_size = 0);
+void qkv_split_heads(const __half* qkv, __half* q, __half* k, __half* v, int T, int n_heads,
+                     int head_dim, hipStream_t stream = 0);
+void qkv_split_heads_gqa(const __half* qkv, __half* q, __half* k, __half* v, int T, int n_q,
+                         int n_kv, int head_dim, hipStream_t stream = 0);
+void merge_heads(const __half* heads, __half* out, int T, int n_heads, int head_dim,
+                 hipStream_t stream = 0);
 
 // Additive fused entry points (no single reference counterpart).
 void rms_norm_quant(const __half* x, const __half* weight, float eps, const __half* smooth_inv,

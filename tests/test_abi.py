@@ -44,7 +44,9 @@ def test_cpp_mirror_symbols_exported():
                  "fish::ModelLoader::get", "fish::infer_group_size_from_scale",
                  "fish::kernels::gemm_fp16", "fish::kernels::int8_rms_gemm_fp16",
                  "fish::kernels::int8_swiglu_gemm_fp16",
-                 "fish::kernels::int8_silu_mul_gemm_fp16"]:
+                 "fish::kernels::int8_silu_mul_gemm_fp16",
+                 "fish::kernels::prefill_attention_gpu", "fish::kernels::qkv_split_heads",
+                 "fish::kernels::qkv_split_heads_gqa", "fish::kernels::merge_heads"]:
         assert name in out, name
 
 
