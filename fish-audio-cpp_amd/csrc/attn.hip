@@ -205,22 +205,28 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kk], qf[kk], s, 0, 0, 0);
-        // scores rounded to fp16 (the reference stores S in fp16); masked
-        // scores become -inf (weight exp2(-inf) = 0); the max is taken before
-        // scaling (sm_scale > 0 keeps the order)
+        // scores rounded to fp16 (the reference stores S in fp16) and kept
+        // packed: masked scores become -inf (weight exp2(-inf) = 0), the max
+        // runs on packed halves and is taken before scaling (sm_scale > 0
+        // keeps the order), and each weight is exp2(fma(float(s), c1, -m))
+        // with the fp16 score as a mixed-precision fma operand.
+        h2 sp[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = (float)(_Float16)s[i];
+        for (int j = 0; j < 8; ++j) sp[j] = h2{(_Float16)s[2 * j], (_Float16)s[2 * j + 1]};
         if (!full) {
             const int kbase = kb * kAttnTile + 4 * hh;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int j = kbase + 8 * (i >> 2) + (i & 3);
-                s[i] = (j <= qi && j >= left) ? s[i] : -__builtin_inff();
+                if (!(j <= qi && j >= left)) sp[i >> 1][i & 1] = -__builtin_inff16();
             }
         }
-        float mloc = s[0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
+        h2 mx = __builtin_elementwise_max(__builtin_elementwise_max(sp[0], sp[1]),
+                                          __builtin_elementwise_max(sp[2], sp[3]));
+        mx = __builtin_elementwise_max(mx, __builtin_elementwise_max(
+                                               __builtin_elementwise_max(sp[4], sp[5]),
+                                               __builtin_elementwise_max(sp[6], sp[7])));
+        float mloc = fmaxf((float)mx[0], (float)mx[1]);
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * c1;
         const bool grow = mloc > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -235,7 +241,8 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         h8 pb[2];
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-            pb[i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c1, -m_run));
+            pb[i >> 3][i & 7] = (_Float16)__builtin_amdgcn_exp2f(
+                __builtin_fmaf((float)sp[i >> 1][i & 1], c1, -m_run));
         // l_run sums the fp16 weights the V product uses (v_dot2: exact pairs)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
