@@ -95,6 +95,9 @@ CASES = [
     (64, 6, 2, 32, 1, 1.0),         # window 1: each query sees itself; 3 heads per group
     (40, 2, 1, 40, 0, 1.0),         # D padded to 64
     (300, 4, 1, 128, 0, 3.0),       # large scores (sharp softmax)
+    (70, 16, 2, 64, 0, 1.0),        # 8 heads per group: two workgroups per tile
+    (45, 12, 2, 128, 0, 1.0),       # 6 heads per group: the second one half idle
+    (1000, 8, 2, 128, 256, 1.0),    # long window, many fully visible blocks
 ]
 
 
