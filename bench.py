@@ -344,6 +344,18 @@ def attention_side(torch, ops):
     out["prefill_attn_t2048_us"] = round(us, 2)
     out["prefill_attn_t2048_TFLOPs"] = round(fl / (us * 1e-6) / 1e12, 1)
     out["prefill_attn_t2048_frac_fp16_peak"] = round(fl / (us * 1e-6) / 1e12 / FP16_PEAK_TFLOPS, 4)
+    # the DAC transformer's attention (dac_engine.cc:1258-1288): MHA, 16
+    # heads of 64, sliding window 128, here at T = 2048
+    Th, Hh, Dh, Wh = 2048, 16, 64, 128
+    qd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
+    kd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
+    vd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
+    od = torch.empty_like(qd)
+    us = graph_us_per_call(
+        torch, [lambda: ops.prefill_attention(qd, kd, vd, 0.125, window=Wh, out=od)] * 4, reps=5)
+    fl = 4.0 * Dh * Hh * sum(min(i + 1, Wh) for i in range(Th))
+    out["dac_attn_t2048_w128_us"] = round(us, 2)
+    out["dac_attn_t2048_w128_TFLOPs"] = round(fl / (us * 1e-6) / 1e12, 1)
     us = graph_us_per_call(torch, [lambda: ops.qkv_split_heads_gqa(qkv, n_q, n_kv, D)] * 4)
     out["qkv_split_t2048_us"] = round(us, 2)
     out["qkv_split_t2048_GBs"] = round(2 * qkv.numel() * 2 / (us * 1e-6) / 1e9, 1)

@@ -56,9 +56,13 @@ __device__ __forceinline__ int vt_pos(int o) {
     return 16 * (o >> 4) + 8 * ((o & 7) >> 2) + 4 * ((o >> 3) & 1) + (o & 3);
 }
 
-// One workgroup: KV head `g`, query heads g * gs + chunk * 4 + (wave & 3),
-// queries q0 .. q0 + 31; DP = head dim rounded up to 32 (D % 8 == 0,
-// D <= DP).  The tile's key blocks are split in two halves: waves 0-3 take the
+// One workgroup: KV head `g` and four (query head, 32-query tile) pairs of
+// its group -- four heads of one tile when the group size allows, else two
+// heads x two tiles or one head x four tiles, so no wave idles for the
+// DualAR (4 heads per group) or the DAC (1) layouts.  DP = head dim rounded
+// up to 32 (D % 8 == 0, D <= DP).  The workgroup's key blocks (the union of
+// its tiles' ranges; each wave skips blocks outside its own) are split in two
+// halves: waves 0-3 take the
 // first, waves 4-7 the second (each half with its own double-buffered K / V^T
 // blocks in LDS and its own online softmax), and the halves are merged
 // through LDS at the end.  Splitting the key range halves the serial chain of
@@ -76,7 +80,7 @@ template <int DP>
 __global__ void __launch_bounds__(2 * kAttnWaves * 64, 1)
 attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                  const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
-                 int T, int D, float sm_scale, int window, int chunks, int n_qb) {
+                 int T, int D, float sm_scale, int window, int hpw, int R, int n_qb) {
     constexpr int KS = DP + 8;            // K row stride in LDS (halves)
     constexpr int VS = kAttnTile + 8;     // V^T row stride in LDS (halves)
     constexpr int NC = 4 * DP;            // 16-byte chunks per block of K
@@ -95,15 +99,20 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     uint16_t* const Ks = lds + half * 2 * (KB + VB);   // [2][KB]
     uint16_t* const Vs = Ks + 2 * KB;                 // [2][VB]
     const int col = lane & 31, hh = lane >> 5;
-    const int gs = n_q / n_kv;
-    // heaviest (last) query tiles first: they have the most key blocks
-    const int qb = n_qb - 1 - (int)(blockIdx.x / (n_kv * chunks));
+    // A workgroup covers hpw query heads of one KV group (hpw = 4, 2 or 1,
+    // the largest that divides the group size) times R <= 4 / hpw consecutive
+    // query tiles: wave w takes head w % hpw of its chunk and tile w / hpw
+    // (waves past R tiles idle).
+    const int gs = n_q / n_kv, chunks = gs / hpw;
+    const int n_grp = (n_qb + R - 1) / R;
+    // heaviest (last) tile groups first: they have the most key blocks
+    const int grp = n_grp - 1 - (int)(blockIdx.x / (n_kv * chunks));
     const int rest = (int)(blockIdx.x % (n_kv * chunks));
     const int g = rest % n_kv, chunk = rest / n_kv;
-    const int hq = chunk * kAttnWaves + wave;        // head index within the group
-    const bool active = hq < gs;
-    const int head = g * gs + (active ? hq : 0);
-    const int q0 = qb * kAttnTile;
+    const int head = g * gs + chunk * hpw + wave % hpw;
+    const int qt = grp * R + wave / hpw;             // this wave's query tile
+    const bool active = wave / hpw < R && qt < n_qb;
+    const int q0 = qt * kAttnTile;
     const int qi = q0 + col;                         // this lane's query
 
     const uint16_t* Kg = k + (int64_t)g * T * D;
@@ -120,9 +129,12 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
             qf[kk] = h8{0, 0, 0, 0, 0, 0, 0, 0};
     }
 
-    const int hi = min(T - 1, q0 + kAttnTile - 1);
-    const int lo = window > 0 ? max(0, q0 - window + 1) : 0;
-    const int kb_lo = lo / kAttnTile, kb_hi = hi / kAttnTile;
+    // key blocks of this wave's tile, and of the workgroup's (all its tiles)
+    const int kb_hi = min(T - 1, q0 + kAttnTile - 1) / kAttnTile;
+    const int kb_lo = (window > 0 ? max(0, q0 - window + 1) : 0) / kAttnTile;
+    const int wg_q0 = grp * R * kAttnTile;
+    const int wg_hi = min(T - 1, min(grp * R + R, n_qb) * kAttnTile - 1) / kAttnTile;
+    const int wg_lo = (window > 0 ? max(0, wg_q0 - window + 1) : 0) / kAttnTile;
     const int left = window > 0 ? qi - window + 1 : 0;   // this lane's first key
     const float c1 = sm_scale * kLog2e;
 
@@ -259,8 +271,8 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 
     // this half's key blocks: the first ceil(n / 2) of the tile's n blocks,
     // or the rest
-    const int nkb = kb_hi - kb_lo + 1, n0 = (nkb + 1) / 2;
-    const int my_lo = half ? kb_lo + n0 : kb_lo, my_n = half ? nkb - n0 : n0;
+    const int nkb = wg_hi - wg_lo + 1, n0 = (nkb + 1) / 2;
+    const int my_lo = half ? wg_lo + n0 : wg_lo, my_n = half ? nkb - n0 : n0;
     if (my_n > 0) {
         load_block(my_lo);
         store_block(0);
@@ -273,7 +285,7 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
             store_block(buf ^ 1);
             if (it + 2 < my_n) load_block(kb + 2);
         }
-        if (active && it < my_n) {
+        if (active && it < my_n && kb >= kb_lo && kb <= kb_hi) {
             // every key of the block visible to all 32 queries of the tile
             const bool full = kb * kAttnTile + kAttnTile - 1 <= q0 &&
                               (window <= 0 || kb * kAttnTile >= q0 + kAttnTile - window);
@@ -377,7 +389,7 @@ inline unsigned blocks_for(int64_t n, int threads) {
 template <int DP>
 hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
-                            int window, int chunks, int n_qb, hipStream_t stream) {
+                            int window, int hpw, int R, int n_qb, hipStream_t stream) {
     constexpr int lds = attn_lds_bytes<DP>();
     static_assert(lds >= 4 * 64 * (DP / 2 + 2) * 4, "merge area exceeds the block buffers");
     static const hipError_t attr = hipFuncSetAttribute(
@@ -385,7 +397,7 @@ hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, con
         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
     attention_kernel<DP><<<grid, 2 * kAttnWaves * 64, lds, stream>>>(
-        q, k, v, out, n_q, n_kv, T, D, sm_scale, window, chunks, n_qb);
+        q, k, v, out, n_q, n_kv, T, D, sm_scale, window, hpw, R, n_qb);
     return hipGetLastError();
 }
 
@@ -397,19 +409,25 @@ hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const 
                                     uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
                                     int window, hipStream_t stream) {
     const int gs = n_q / n_kv;
-    const int chunks = (gs + kAttnWaves - 1) / kAttnWaves;
+    const int hpw = gs % 4 == 0 ? 4 : gs % 2 == 0 ? 2 : 1;   // heads per workgroup
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;
-    const dim3 grid((unsigned)(n_qb * n_kv * chunks));
+    // query tiles per workgroup: fill all four wave slots unless that leaves
+    // fewer workgroups than CUs (measured: MHA with 8 heads at T = 1024 is
+    // faster with idle waves and 4x the workgroups)
+    int R = kAttnWaves / hpw;
+    auto wgs = [&](int r) { return (int64_t)((n_qb + r - 1) / r) * n_kv * (gs / hpw); };
+    while (R > 1 && wgs(R) < 256) R /= 2;
+    const dim3 grid((unsigned)wgs(R));
     switch (attention_padded_dim(D)) {
         case 32:
             return launch_attention<32>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                        chunks, n_qb, stream);
+                                        hpw, R, n_qb, stream);
         case 64:
             return launch_attention<64>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                        chunks, n_qb, stream);
+                                        hpw, R, n_qb, stream);
         case 128:
             return launch_attention<128>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                         chunks, n_qb, stream);
+                                         hpw, R, n_qb, stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -98,6 +98,9 @@ CASES = [
     (70, 16, 2, 64, 0, 1.0),        # 8 heads per group: two workgroups per tile
     (45, 12, 2, 128, 0, 1.0),       # 6 heads per group: the second one half idle
     (1000, 8, 2, 128, 256, 1.0),    # long window, many fully visible blocks
+    # grids large enough that a workgroup packs several query tiles:
+    (1024, 32, 32, 64, 128, 1.0),   # DAC-style MHA, window 128: 1 head x 4 tiles
+    (512, 64, 32, 64, 0, 1.0),      # 2 heads per group: 2 heads x 2 tiles
 ]
 
 
