@@ -3,10 +3,10 @@
 //
 // Reference: src/kernels/prefill_attention.cu.  The reference materialises the
 // fp16 score matrix S = Q K^T [n_q, T, T] with a batched GEMM, runs a masked
-// row softmax in place and a per-row S V product.  Here one kernel keeps a
-// 32-query tile of each of the group's query heads on chip and streams 32-key
-// blocks of K and V through LDS, with the running-max (online) softmax, so the
-// T x T matrix never reaches HBM.  Numerics follow the reference where they
+// row softmax in place and a per-row S V product.  Here one kernel keeps
+// 32-query tiles of query heads that share a KV head on chip and streams
+// 32-key blocks of K and V through LDS, with the running-max (online) softmax,
+// so the T x T matrix never reaches HBM.  Numerics follow the reference where they
 // are observable: every score is rounded to fp16 before it is scaled
 // (prefill_attention.cu:276-290 writes S in fp16, :160-162 reads it back),
 // masked keys get weight 0, probabilities enter the V product as fp16 and the
@@ -34,11 +34,10 @@ namespace fa {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int kAttnWaves = 4;      // query heads of one KV group per workgroup
+constexpr int kAttnWaves = 4;      // (query head, tile) pairs per workgroup
 constexpr int kAttnTile = 32;      // queries per wave and keys per block
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMasked = -1e30f;  // the reference's mask value (prefill_attention.cu:161)
@@ -62,10 +61,9 @@ __device__ __forceinline__ int vt_pos(int o) {
 // DualAR (4 heads per group) or the DAC (1) layouts.  DP = head dim rounded
 // up to 32 (D % 8 == 0, D <= DP).  The workgroup's key blocks (the union of
 // its tiles' ranges; each wave skips blocks outside its own) are split in two
-// halves: waves 0-3 take the
-// first, waves 4-7 the second (each half with its own double-buffered K / V^T
-// blocks in LDS and its own online softmax), and the halves are merged
-// through LDS at the end.  Splitting the key range halves the serial chain of
+// halves: waves 0-3 take the first, waves 4-7 the second (each half with its
+// own double-buffered K / V^T blocks in LDS and its own online softmax), and
+// the halves are merged through LDS at the end.  Splitting the key range halves the serial chain of
 // the tiles next to the diagonal of long sequences, which would otherwise
 // set the kernel's duration.  Within a half, the block after next is in
 // flight in registers while the current one is multiplied (one barrier per
