@@ -263,10 +263,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 // Direct-to-LDS loads: lane i's data lands at lds + i * size.  m0 holds the
 // wave-uniform LDS base; no compiler-generated code in these kernels uses m0.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
-}
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
                  :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
