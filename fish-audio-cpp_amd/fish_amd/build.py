@@ -67,6 +67,22 @@ def build_library(verbose=False):
     return LIB_PATH
 
 
+TEST_DRIVER_SRC = os.path.join(REPO_ROOT, "tests", "cxx", "engine_prefill.cpp")
+TEST_DRIVER = os.path.join(LIB_DIR, "engine_prefill")
+
+
+def build_test_driver(verbose=False):
+    """The C++ test driver (tests/cxx/engine_prefill.cpp): the engine's
+    prefill attention block through the C++ mirror, linked to the library."""
+    out = _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-x", "hip",
+                "-I", os.path.join(PKG_ROOT, "include"), TEST_DRIVER_SRC,
+                "-L", LIB_DIR, "-lfish_w8a8", "-Wl,-rpath,$ORIGIN", "-o", TEST_DRIVER + ".tmp"])
+    os.replace(TEST_DRIVER + ".tmp", TEST_DRIVER)
+    if verbose and out.strip():
+        print(out)
+    return TEST_DRIVER
+
+
 def build_oracle(verbose=False):
     out = _run(["make", "-s", "-C", ORACLE_DIR])
     if verbose and out.strip():
@@ -76,5 +92,6 @@ def build_oracle(verbose=False):
 
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    print(build_test_driver(verbose=True))
     print(build_oracle(verbose=True))
     sys.exit(0)
