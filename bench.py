@@ -344,6 +344,10 @@ def attention_side(torch, ops):
     out["prefill_attn_t2048_us"] = round(us, 2)
     out["prefill_attn_t2048_TFLOPs"] = round(fl / (us * 1e-6) / 1e12, 1)
     out["prefill_attn_t2048_frac_fp16_peak"] = round(fl / (us * 1e-6) / 1e12 / FP16_PEAK_TFLOPS, 4)
+    mt = torch.empty((T, n_q * D), device="cuda", dtype=torch.float16)
+    us = graph_us_per_call(
+        torch, [lambda: ops.prefill_attention_merged(q, k, v, sc, out=mt)] * 4, reps=5)
+    out["prefill_attn_merged_t2048_us"] = round(us, 2)
     # the DAC transformer's attention (dac_engine.cc:1258-1288): MHA, 16
     # heads of 64, sliding window 128, here at T = 2048
     Th, Hh, Dh, Wh = 2048, 16, 64, 128

@@ -546,11 +546,10 @@ int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int
     return FA_OK;
 }
 
-int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
-                         void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
-                         void* stream, int window_size) {
-    const char* fn = "fa_prefill_attention";
-    (void)workspace;   // the fused kernel keeps scores on chip and needs no scratch
+namespace {
+int prefill_attention(const char* fn, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                      uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                      void* stream, int window_size, bool token_major) {
     g_err.clear();
     if (T < 0 || n_q <= 0 || n_kv <= 0 || D <= 0)
         return fail(FA_ERR_INVALID_ARG, "%s: bad n_q=%d n_kv=%d T=%d D=%d", fn, n_q, n_kv, T, D);
@@ -568,8 +567,24 @@ int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
         return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 16-byte aligned", fn);
     FA_HIP(fa::launch_prefill_attention(q, k, v, out, n_q, n_kv, T, D, sm_scale, window_size,
-                                        (hipStream_t)stream));
+                                        token_major, (hipStream_t)stream));
     return FA_OK;
+}
+}  // namespace
+
+int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                         void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
+                         void* stream, int window_size) {
+    (void)workspace;   // the fused kernel keeps scores on chip and needs no scratch
+    return prefill_attention("fa_prefill_attention", q, k, v, out, n_q, n_kv, T, D, sm_scale,
+                             stream, window_size, false);
+}
+
+int fa_prefill_attention_merged(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                void* stream, int window_size) {
+    return prefill_attention("fa_prefill_attention_merged", q, k, v, out, n_q, n_kv, T, D,
+                             sm_scale, stream, window_size, true);
 }
 
 int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_size, void* stream) {

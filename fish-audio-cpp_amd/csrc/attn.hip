@@ -78,7 +78,8 @@ template <int DP>
 __global__ void __launch_bounds__(2 * kAttnWaves * 64, 1)
 attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                  const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q, int n_kv,
-                 int T, int D, float sm_scale, int window, int hpw, int R, int n_qb) {
+                 int T, int D, float sm_scale, int window, int hpw, int R, int n_qb,
+                 bool token_major) {
     constexpr int KS = DP + 8;            // K row stride in LDS (halves)
     constexpr int VS = kAttnTile + 8;     // V^T row stride in LDS (halves)
     constexpr int NC = 4 * DP;            // 16-byte chunks per block of K
@@ -312,7 +313,10 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float l_lane = l_run * f0 + red[64] * f1;
     const float l_tot = l_lane + __shfl_xor(l_lane, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t* orow = out + ((int64_t)head * T + qi) * D;
+    // head-major [n_q, T, D], or token-major [T, n_q D] (the merged layout
+    // merge_heads would produce)
+    uint16_t* orow = out + (token_major ? ((int64_t)qi * n_q + head) * D
+                                        : ((int64_t)head * T + qi) * D);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -387,7 +391,8 @@ inline unsigned blocks_for(int64_t n, int threads) {
 template <int DP>
 hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
-                            int window, int hpw, int R, int n_qb, hipStream_t stream) {
+                            int window, int hpw, int R, int n_qb, bool token_major,
+                            hipStream_t stream) {
     constexpr int lds = attn_lds_bytes<DP>();
     static_assert(lds >= 4 * 64 * (DP / 2 + 2) * 4, "merge area exceeds the block buffers");
     static const hipError_t attr = hipFuncSetAttribute(
@@ -395,7 +400,7 @@ hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, con
         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
     attention_kernel<DP><<<grid, 2 * kAttnWaves * 64, lds, stream>>>(
-        q, k, v, out, n_q, n_kv, T, D, sm_scale, window, hpw, R, n_qb);
+        q, k, v, out, n_q, n_kv, T, D, sm_scale, window, hpw, R, n_qb, token_major);
     return hipGetLastError();
 }
 
@@ -405,7 +410,7 @@ int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 
 
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                     uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
-                                    int window, hipStream_t stream) {
+                                    int window, bool token_major, hipStream_t stream) {
     const int gs = n_q / n_kv;
     const int hpw = gs % 4 == 0 ? 4 : gs % 2 == 0 ? 2 : 1;   // heads per workgroup
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;
@@ -419,13 +424,13 @@ hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const 
     switch (attention_padded_dim(D)) {
         case 32:
             return launch_attention<32>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                        hpw, R, n_qb, stream);
+                                        hpw, R, n_qb, token_major, stream);
         case 64:
             return launch_attention<64>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                        hpw, R, n_qb, stream);
+                                        hpw, R, n_qb, token_major, stream);
         case 128:
             return launch_attention<128>(grid, q, k, v, out, n_q, n_kv, T, D, sm_scale, window,
-                                         hpw, R, n_qb, stream);
+                                         hpw, R, n_qb, token_major, stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -209,7 +209,8 @@ hipError_t launch_gemm_f16_generic(const uint16_t* W, const uint16_t* X, uint16_
 int attention_padded_dim(int D);
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                     uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
-                                    int window, hipStream_t stream);
+                                    int window, bool token_major,
+                                    hipStream_t stream);
 hipError_t launch_qkv_split(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T,
                             int n_q, int n_kv, int D, bool vec, hipStream_t stream);
 hipError_t launch_merge_heads(const uint16_t* heads, uint16_t* out, int T, int H, int D, bool vec,

@@ -112,4 +112,11 @@ void merge_heads(const __half* heads, __half* out, int T, int n_heads, int head_
     check(fa_merge_heads(u16(heads), u16(out), T, n_heads, head_dim, stream));
 }
 
+void prefill_attention_merged(const __half* q, const __half* k, const __half* v, __half* out,
+                              int n_q, int n_kv, int T, int D, float sm_scale, hipStream_t stream,
+                              int window_size) {
+    check(fa_prefill_attention_merged(u16(q), u16(k), u16(v), u16(out), n_q, n_kv, T, D, sm_scale,
+                                      stream, window_size));
+}
+
 }  // namespace fish::kernels

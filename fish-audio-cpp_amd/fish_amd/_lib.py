@@ -87,6 +87,7 @@ SIGNATURES = {
     "fa_qkv_split_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_merge_heads": (_i, [_p, _p, _i, _i, _i, _p]),
     "fa_prefill_attention": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i]),
+    "fa_prefill_attention_merged": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i]),
     "fa_workspace_reserve": (_i, [_i, _i, _i, _i, _p]),
     "fa_workspace_release": (_i, []),
     "fa_chain_create": (_i, [ctypes.POINTER(ChainStep), _i, _i, ctypes.POINTER(_p)]),

@@ -237,6 +237,19 @@ def qkv_split_heads_gqa(qkv, n_q, n_kv, head_dim):
     return q, k, v
 
 
+def prefill_attention_merged(q, k, v, sm_scale, window=0, out=None):
+    """prefill_attention then merge_heads in one launch -> out [T, n_q D]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, torch.float16, n)
+    n_q, T, D = q.shape
+    n_kv = k.shape[0]
+    if out is None:
+        out = torch.empty((T, n_q * D), dtype=torch.float16, device=q.device)
+    check(lib().fa_prefill_attention_merged(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_q, n_kv, T, D,
+                                            float(sm_scale), _stream(), int(window)))
+    return out
+
+
 def merge_heads(heads, out=None):
     """Head-major fp16 [H, T, D] -> token-major [T, H D] (prefill_attention.cu:68-86)."""
     _need(heads, torch.float16, "heads")

@@ -40,6 +40,11 @@ void qkv_split_heads_gqa(const __half* qkv, __half* q, __half* k, __half* v, int
                          int n_kv, int head_dim, hipStream_t stream = 0);
 void merge_heads(const __half* heads, __half* out, int T, int n_heads, int head_dim,
                  hipStream_t stream = 0);
+// prefill_attention_gpu + merge_heads in one launch (fa_prefill_attention_merged):
+// out token-major [T, n_q * D].
+void prefill_attention_merged(const __half* q, const __half* k, const __half* v, __half* out,
+                              int n_q, int n_kv, int T, int D, float sm_scale,
+                              hipStream_t stream = 0, int window_size = 0);
 
 // Additive fused entry points (no single reference counterpart).
 void rms_norm_quant(const __half* x, const __half* weight, float eps, const __half* smooth_inv,

@@ -210,6 +210,13 @@ int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int
 int fa_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                          void* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
                          void* stream, int window_size);
+/* prefill_attention_gpu followed by merge_heads (dual_ar_engine.cc:499-502),
+ * as one launch: the same attention, written token-major, out [T, n_q D]
+ * (bit-identical to fa_prefill_attention then fa_merge_heads).  Additive: no
+ * single reference counterpart. */
+int fa_prefill_attention_merged(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
+                                void* stream, int window_size);
 
 /* ------------------------------------------------------------------------ */
 /* Decode chain: a sequence of one-token W8A8 linears as one launch.          */

@@ -46,7 +46,8 @@ def test_cpp_mirror_symbols_exported():
                  "fish::kernels::int8_swiglu_gemm_fp16",
                  "fish::kernels::int8_silu_mul_gemm_fp16",
                  "fish::kernels::prefill_attention_gpu", "fish::kernels::qkv_split_heads",
-                 "fish::kernels::qkv_split_heads_gqa", "fish::kernels::merge_heads"]:
+                 "fish::kernels::qkv_split_heads_gqa", "fish::kernels::merge_heads",
+                 "fish::kernels::prefill_attention_merged"]:
         assert name in out, name
 
 

@@ -183,3 +183,16 @@ def test_prefill_attention_stream_and_repeat():
         b = ops.prefill_attention(dq, dk, dvv, 0.088)
     s.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,n_q,n_kv,D,window", [(77, 32, 8, 128, 0), (300, 8, 8, 64, 128),
+                                                 (40, 6, 2, 40, 0)])
+def test_prefill_attention_merged_equals_attention_then_merge(T, n_q, n_kv, D, window):
+    """The fused token-major store gives exactly merge_heads(attention)."""
+    rng = np.random.default_rng(T + 5)
+    q, k, v = ref.qkv_split_gqa(qkv_rand(rng, T, n_q, n_kv, D), n_q, n_kv, D)
+    dq, dk, dvv = dev(q), dev(k), dev(v)
+    sep = ops.merge_heads(ops.prefill_attention(dq, dk, dvv, 1.0 / np.sqrt(D), window))
+    fused = ops.prefill_attention_merged(dq, dk, dvv, 1.0 / np.sqrt(D), window)
+    torch.cuda.synchronize()
+    assert torch.equal(sep, fused)
