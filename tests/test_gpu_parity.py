@@ -35,7 +35,8 @@ def _device():
 
 
 def dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    # a copy: arrays viewing a read-only memory map are not writable
+    return torch.from_numpy(np.array(a, copy=True, order="C")).cuda()
 
 
 def host(t):
