@@ -555,17 +555,16 @@ int prefill_attention(const char* fn, const uint16_t* q, const uint16_t* k, cons
         return fail(FA_ERR_INVALID_ARG, "%s: bad n_q=%d n_kv=%d T=%d D=%d", fn, n_q, n_kv, T, D);
     if (n_q % n_kv != 0)
         return fail(FA_ERR_INVALID_ARG, "%s: n_q=%d is not a multiple of n_kv=%d", fn, n_q, n_kv);
-    if (D % 8 != 0 || fa::attention_padded_dim(D) == 0)
-        return fail(FA_ERR_INVALID_ARG, "%s: head dim %d unsupported (D %% 8 == 0, D <= 128)", fn,
-                    D);
-    if (!(sm_scale > 0.0f) || sm_scale > 3.0e38f)
-        return fail(FA_ERR_INVALID_ARG, "%s: sm_scale must be positive and finite", fn);
+    if (D > fa::attention_max_dim())
+        return fail(FA_ERR_INVALID_ARG, "%s: head dim %d above %d", fn, D, fa::attention_max_dim());
+    if (!(sm_scale == sm_scale) || sm_scale > 3.0e38f || sm_scale < -3.0e38f)
+        return fail(FA_ERR_INVALID_ARG, "%s: sm_scale must be finite", fn);
     if ((int64_t)n_q * T * D > INT32_MAX)
         return fail(FA_ERR_INVALID_ARG, "%s: q larger than 2^31 elements", fn);
     if (T == 0) return FA_OK;
     if (!q || !k || !v || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-        return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 16-byte aligned", fn);
+    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 1)
+        return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 2-byte aligned", fn);
     FA_HIP(fa::launch_prefill_attention(q, k, v, out, n_q, n_kv, T, D, sm_scale, window_size,
                                         token_major, (hipStream_t)stream));
     return FA_OK;

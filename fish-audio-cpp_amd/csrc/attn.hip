@@ -338,6 +338,71 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
         }
 }
 
+// Any-shape attention (head dim not a multiple of 8 or above 128, a
+// non-positive scale, or buffers not 16-byte aligned): one wave per (query
+// head, query), three passes over the query's visible keys, in the
+// reference's order of operations -- the row max of the fp16-rounded, scaled
+// scores; their exp-sum; then P = fp16(exp(v - max) * (1 / sum)) and
+// O[d] = fp16(sum_j float(P_j) * float(V_jd)) with the fma chain in key order
+// (causal_softmax_kernel and sgemv_kernel, prefill_attention.cu:141-224,
+// 325-349).  Lanes take keys for the scores and head-dim columns for O.
+// Correct for every shape the API accepts; not a fast path.
+constexpr int kGenMaxD = 512;
+
+__global__ void __launch_bounds__(256)
+attention_generic_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                         const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q,
+                         int n_kv, int T, int D, float sm_scale, int window, bool token_major) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t idx = (int64_t)blockIdx.x * 4 + wave;
+    if (idx >= (int64_t)n_q * T) return;          // whole wave; no barriers below
+    const int head = (int)(idx / T), i = (int)(idx % T);
+    const int g = head / (n_q / n_kv);
+    const uint16_t* qr = q + ((int64_t)head * T + i) * D;
+    const uint16_t* Kg = k + (int64_t)g * T * D;
+    const uint16_t* Vg = v + (int64_t)g * T * D;
+    const int left = window > 0 ? max(0, i - window + 1) : 0;
+    auto score = [&](int j) {        // float(fp16(q . k_j)) * sm_scale
+        const uint16_t* kr = Kg + (int64_t)j * D;
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) acc = __builtin_fmaf(h2f(qr[d]), h2f(kr[d]), acc);
+        return h2f(f2h(acc)) * sm_scale;
+    };
+    float mx = -__builtin_inff();
+    for (int j = left + lane; j <= i; j += 64) mx = fmaxf(mx, score(j));
+    mx = subgroup_max<64>(mx);
+    float sum = 0.0f;
+    for (int j = left + lane; j <= i; j += 64) sum += expf(score(j) - mx);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    float o[kGenMaxD / 64];
+#pragma unroll
+    for (int r = 0; r < kGenMaxD / 64; ++r) o[r] = 0.0f;
+    for (int j0 = left; j0 <= i; j0 += 64) {
+        const int j = j0 + lane;
+        const float p = j <= i ? h2f(f2h(expf(score(j) - mx) * inv)) : 0.0f;
+        const int nj = min(64, i - j0 + 1);
+        for (int t = 0; t < nj; ++t) {       // t is wave-uniform: a lane read
+            const float pj =
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), t));
+            const uint16_t* vr = Vg + (int64_t)(j0 + t) * D;
+#pragma unroll
+            for (int r = 0; r < kGenMaxD / 64; ++r) {
+                const int d = lane + 64 * r;
+                if (d < D) o[r] = __builtin_fmaf(pj, h2f(vr[d]), o[r]);
+            }
+        }
+    }
+    uint16_t* orow = out + (token_major ? ((int64_t)i * n_q + head) * D
+                                        : ((int64_t)head * T + i) * D);
+#pragma unroll
+    for (int r = 0; r < kGenMaxD / 64; ++r) {
+        const int d = lane + 64 * r;
+        if (d < D) orow[d] = f2h(o[r]);
+    }
+}
+
 // Fused QKV [T, (n_q + 2 n_kv) D] -> q [n_q, T, D], k / v [n_kv, T, D]; one
 // thread per VEC halves (VEC = 8 when D % 8 == 0 and every buffer is 16-byte
 // aligned, else 1).
@@ -408,9 +473,19 @@ hipError_t launch_attention(dim3 grid, const uint16_t* q, const uint16_t* k, con
 
 int attention_padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
 
+int attention_max_dim() { return kGenMaxD; }
+
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                     uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
                                     int window, bool token_major, hipStream_t stream) {
+    const bool fast = D % 8 == 0 && attention_padded_dim(D) != 0 && sm_scale > 0.0f &&
+                      (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) == 0;
+    if (!fast) {
+        const int64_t rows = (int64_t)n_q * T;
+        attention_generic_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, stream>>>(
+            q, k, v, out, n_q, n_kv, T, D, sm_scale, window, token_major);
+        return hipGetLastError();
+    }
     const int gs = n_q / n_kv;
     const int hpw = gs % 4 == 0 ? 4 : gs % 2 == 0 ? 2 : 1;   // heads per workgroup
     const int n_qb = (T + kAttnTile - 1) / kAttnTile;

@@ -207,6 +207,7 @@ hipError_t launch_gemm_f16_generic(const uint16_t* W, const uint16_t* X, uint16_
 // Prefill attention side (attn.hip).  attention_padded_dim gives the head dim
 // the fused attention kernel is instantiated for (32, 64 or 128), 0 if D > 128.
 int attention_padded_dim(int D);
+int attention_max_dim();   // head dims above it are rejected
 hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                     uint16_t* out, int n_q, int n_kv, int T, int D, float sm_scale,
                                     int window, bool token_major,

@@ -201,9 +201,10 @@ int fa_merge_heads(const uint16_t* heads, uint16_t* out, int T, int n_heads, int
  * prefill_attention.cu:226-349): causal GQA attention, query head h reading
  * KV head h / (n_q / n_kv); window_size > 0 limits query i to keys
  * i - window_size + 1 .. i.  q / out [n_q, T, D], k / v [n_kv, T, D], fp16,
- * head-major, 16-byte aligned; D % 8 == 0 and D <= 128; n_q % n_kv == 0;
- * sm_scale > 0.  One fused kernel: the T x T scores stay on chip, so
- * `workspace` is not used (it may be NULL; the reference's cuBLAS handle has no
+ * head-major; n_q % n_kv == 0; D <= 512; any finite sm_scale.  The fused
+ * kernel serves D % 8 == 0, D <= 128, sm_scale > 0 and 16-byte aligned
+ * buffers; anything else runs an exact-order any-shape kernel (slower).
+ * Either way the T x T scores stay on chip, so `workspace` is not used (it may be NULL; the reference's cuBLAS handle has no
  * counterpart).  Results agree with the reference within the order of fp32
  * sums (scores are rounded to fp16 before scaling, probabilities enter the V
  * product as fp16). */

@@ -96,14 +96,15 @@ def test_invalid_arguments_rejected_without_device():
     # attention side: GQA ratio, head dim, alignment, empty sequence
     assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 6, 4, 8, 64, 0.1, None, 0) == 1
     assert "multiple" in l.fa_last_error().decode()
-    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 136, 0.1, None,
+    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 520, 0.1, None,
                                   0) == 1
-    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 60, 0.1, None, 0) == 1
-    odd = ctypes.c_void_p(18)
+    assert "head dim" in l.fa_last_error().decode()
+    odd = ctypes.c_void_p(17)
     assert l.fa_prefill_attention(odd, dummy, dummy, dummy, None, 8, 4, 8, 64, 0.1, None, 0) == 1
     assert "aligned" in l.fa_last_error().decode()
     assert l.fa_prefill_attention(None, None, None, None, None, 8, 4, 0, 64, 0.1, None, 0) == 0
-    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 64, 0.0, None, 0) == 1
+    assert l.fa_prefill_attention(dummy, dummy, dummy, dummy, None, 8, 4, 8, 64, float("nan"),
+                                  None, 0) == 1
     assert "sm_scale" in l.fa_last_error().decode()
     assert l.fa_qkv_split_heads_gqa(None, dummy, dummy, dummy, 4, 8, 4, 64, None) == 1
     assert l.fa_qkv_split_heads(None, None, None, None, 0, 8, 64, None) == 0

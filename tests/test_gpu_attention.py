@@ -197,3 +197,42 @@ def test_prefill_attention_merged_equals_attention_then_merge(T, n_q, n_kv, D, w
     fused = ops.prefill_attention_merged(dq, dk, dvv, 1.0 / np.sqrt(D), window)
     torch.cuda.synchronize()
     assert torch.equal(sep, fused)
+
+
+@pytest.mark.parametrize("T,n_q,n_kv,D,window,sm", [
+    (37, 4, 2, 12, 0, None),       # D % 8 != 0
+    (60, 4, 1, 136, 0, None),      # D > 128
+    (45, 2, 2, 256, 9, None),      # D 256, window
+    (50, 4, 2, 64, 0, -0.125),     # negative scale (max taken after scaling)
+    (33, 2, 1, 64, 0, 0.0),        # zero scale: uniform weights
+])
+def test_prefill_attention_any_shape(T, n_q, n_kv, D, window, sm):
+    """Shapes outside the fused kernel (head dim not a multiple of 8 or above
+    128, a non-positive scale) run the any-shape kernel, against the oracle
+    within the same bound."""
+    what = "generic T=%d n_q=%d n_kv=%d D=%d window=%d sm=%r" % (T, n_q, n_kv, D, window, sm)
+    print(what, flush=True)
+    rng = np.random.default_rng(T * 3 + D)
+    q, k, v = ref.qkv_split_gqa(qkv_rand(rng, T, n_q, n_kv, D), n_q, n_kv, D)
+    check_attention(q, k, v, 1.0 / np.sqrt(D) if sm is None else sm, window, what)
+
+
+def test_prefill_attention_unaligned_buffers():
+    """Buffers offset by one fp16 element (2-byte aligned only) take the
+    any-shape kernel and give the same result within the bound."""
+    rng = np.random.default_rng(77)
+    T, n_q, n_kv, D = 40, 4, 2, 64
+    q, k, v = ref.qkv_split_gqa(qkv_rand(rng, T, n_q, n_kv, D), n_q, n_kv, D)
+    def off(a):
+        t = torch.empty(a.size + 1, dtype=torch.float16, device="cuda")
+        t[1:] = dev(a.reshape(-1))
+        return t
+    dq, dk, dvv, do = off(q), off(k), off(v), torch.zeros(q.size + 1, dtype=torch.float16,
+                                                          device="cuda")
+    l = _lib.lib()
+    sc = 1.0 / np.sqrt(D)
+    _lib.check(l.fa_prefill_attention(dq.data_ptr() + 2, dk.data_ptr() + 2, dvv.data_ptr() + 2,
+                                      do.data_ptr() + 2, None, n_q, n_kv, T, D, sc, None, 0))
+    got = host(do)[1:].reshape(n_q, T, D).astype(np.float64)
+    want, aw = ref.prefill_attention(q, k, v, sc)
+    assert np.all(np.abs(got - want) <= ref.attention_tolerance(want, aw))
