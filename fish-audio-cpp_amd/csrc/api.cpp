@@ -83,9 +83,12 @@ int grow(void** p, size_t* have, size_t need, hipStream_t stream) {
 
 int eff_group(int K, int g) { return (g <= 0 || g > K) ? K : g; }
 
+// tables: device memory of gemm_pipe_tables_bytes(M, N, G) for the prefill
+// kernels' scale tables, or nullptr to use (and grow) this thread's scratch.
 int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, int g, int G,
                      const int8_t* xq, const float* xs, uint16_t* Y, int32_t* dbg, int row0,
-                     int rows, int tok0, int toks, int M, int N, int K, hipStream_t stream) {
+                     int rows, int tok0, int toks, int M, int N, int K, hipStream_t stream,
+                     float* tables = nullptr) {
     const bool aligned = aligned16(W) && aligned16(xq);
     if (aligned && N <= 16) {
         fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G, false);
@@ -97,18 +100,21 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
     }
     const bool tile = aligned && fa::gemm_tile_ok(M, N, K, g);
     if (tile || (aligned && fa::gemm_pipe_ok(M, N, K, g))) {
-        Workspace* ws = nullptr;
-        int rc = current_ws(&ws);
-        if (rc) return rc;
-        void* p = ws->st;
-        rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(M, N, G), stream);
-        ws->st = (float*)p;
-        if (rc) return rc;
+        if (!tables) {
+            Workspace* ws = nullptr;
+            int rc = current_ws(&ws);
+            if (rc) return rc;
+            void* p = ws->st;
+            rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(M, N, G), stream);
+            ws->st = (float*)p;
+            if (rc) return rc;
+            tables = ws->st;
+        }
         if (tile)
-            FA_HIP(fa::launch_gemm_tile(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks,
+            FA_HIP(fa::launch_gemm_tile(W, w_scale, xq, xs, tables, Y, dbg, row0, rows, tok0, toks,
                                         M, N, K, g, G, stream));
         else
-            FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, ws->st, Y, dbg, row0, rows, tok0, toks,
+            FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, tables, Y, dbg, row0, rows, tok0, toks,
                                         M, N, K, g, G, stream));
         return FA_OK;
     }
@@ -127,6 +133,11 @@ int check_dims(const char* fn, int M, int N, int K) {
     if (M < 0 || N < 0) return fail(FA_ERR_INVALID_ARG, "%s: negative M=%d or N=%d", fn, M, N);
     if (K <= 0) return fail(FA_ERR_INVALID_ARG, "%s: K=%d must be positive", fn, K);
     return FA_OK;
+}
+
+// [a, a + n) and [b, b + m) overlap (fp16 element counts)
+bool overlaps(const uint16_t* a, size_t n, const uint16_t* b, size_t m) {
+    return a && b && a < b + m && b < a + n;
 }
 
 }  // namespace
@@ -186,6 +197,8 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     if (rc) return rc;
     if (M == 0 || N == 0) return FA_OK;
     if (!W || !w_scale || !X || !Y) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (overlaps(Y, (size_t)N * M, X, (size_t)N * K))
+        return fail(FA_ERR_INVALID_ARG, "%s: Y overlaps X", fn);
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
@@ -215,11 +228,6 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
                             s);
 }
 
-// [a, a + n) and [b, b + m) overlap (fp16 element counts)
-static bool overlaps(const uint16_t* a, size_t n, const uint16_t* b, size_t m) {
-    return a && b && a < b + m && b < a + n;
-}
-
 int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
                      const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
                      const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
@@ -236,6 +244,10 @@ int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
     const size_t nk = (size_t)N * (size_t)K;
     if (h_out && (overlaps(h_out, nk, x, nk) || overlaps(h_out, nk, resid, nk)))
         return fail(FA_ERR_INVALID_ARG, "%s: h_out overlaps x or resid", fn);
+    const size_t nm = (size_t)N * (size_t)M;
+    if (overlaps(Y, nm, x, nk) || overlaps(Y, nm, resid, nk) || overlaps(Y, nm, h_out, nk) ||
+        overlaps(Y, nm, gamma, (size_t)K))
+        return fail(FA_ERR_INVALID_ARG, "%s: Y overlaps an input or h_out", fn);
     if (K > 65536) return fail(FA_ERR_INVALID_ARG, "%s: K=%d exceeds 65536", fn, K);
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
@@ -294,6 +306,10 @@ int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_
     const size_t nk = (size_t)N * (size_t)K;
     if (h_out && (overlaps(h_out, nk, x, nk) || overlaps(h_out, nk, resid, nk)))
         return fail(FA_ERR_INVALID_ARG, "%s: h_out overlaps x or resid", fn);
+    const size_t nf = (size_t)N * (size_t)F;
+    if (overlaps(act, nf, x, nk) || overlaps(act, nf, resid, nk) || overlaps(act, nf, h_out, nk) ||
+        overlaps(act, nf, gamma, (size_t)K))
+        return fail(FA_ERR_INVALID_ARG, "%s: act overlaps an input or h_out", fn);
     if (gamma && K > 65536) return fail(FA_ERR_INVALID_ARG, "%s: K=%d exceeds 65536", fn, K);
     hipStream_t s = (hipStream_t)stream;
     const int M = 2 * F;
@@ -340,6 +356,8 @@ int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_si
     if (M == 0 || N == 0) return FA_OK;
     if (!W || !w_scale || !gate || !up || !Y)
         return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (overlaps(Y, (size_t)N * M, gate, (size_t)N * K) || overlaps(Y, (size_t)N * M, up, (size_t)N * K))
+        return fail(FA_ERR_INVALID_ARG, "%s: Y overlaps gate or up", fn);
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
@@ -565,6 +583,9 @@ int prefill_attention(const char* fn, const uint16_t* q, const uint16_t* k, cons
     if (!q || !k || !v || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
     if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 1)
         return fail(FA_ERR_INVALID_ARG, "%s: q, k, v and out must be 2-byte aligned", fn);
+    const size_t nq = (size_t)n_q * T * D, nkv = (size_t)n_kv * T * D;
+    if (overlaps(out, nq, q, nq) || overlaps(out, nq, k, nkv) || overlaps(out, nq, v, nkv))
+        return fail(FA_ERR_INVALID_ARG, "%s: out overlaps q, k or v", fn);
     FA_HIP(fa::launch_prefill_attention(q, k, v, out, n_q, n_kv, T, D, sm_scale, window_size,
                                         token_major, (hipStream_t)stream));
     return FA_OK;

@@ -44,14 +44,34 @@ class Linear:
         return self.W.numel() + 2 * self.scale.numel()
 
 
+def smooth_factors(K, gen):
+    """AWQ-style per-channel smooth_inv (log-normal around 1, fp16), as the
+    reference exporter attaches to every calibrated wqkv / w1 / w3
+    (tools/step2_export_w8a8.py:477)."""
+    z = torch.randn(K, generator=gen, device="cuda").mul_(0.5).clamp_(-1.6, 1.6)
+    return torch.exp(z).half()
+
+
 class DecodeStack:
-    def __init__(self, n_layers=36, g=256, tokens=1, seed=0):
+    """awq=False: synthetic un-calibrated weights; gate_up is the
+    row-interleaved w1 / w3 pair.  awq=True: the calibrated layout a real
+    dual_ar.bin carries -- wqkv, w1 and w3 each with their own smooth_inv
+    (so w1 and w3 see different int8 inputs and stay separate weights)."""
+
+    def __init__(self, n_layers=36, g=256, tokens=1, seed=0, awq=False):
         gen = torch.Generator(device="cuda")
         gen.manual_seed(seed)
-        self.g, self.n, self.T = g, n_layers, tokens
+        self.g, self.n, self.T, self.awq = g, n_layers, tokens, awq
         self.layers = []
         for _ in range(n_layers):
-            lay = {name: Linear(K, N, g, gen) for name, (K, N) in LAYER_SHAPES.items()}
+            if awq:
+                lay = {"qkv": Linear(HIDDEN, 6144, g, gen), "o": Linear(Q_DIM, HIDDEN, g, gen),
+                       "w1": Linear(HIDDEN, FFN, g, gen), "w3": Linear(HIDDEN, FFN, g, gen),
+                       "down": Linear(FFN, HIDDEN, g, gen)}
+                for name in ("qkv", "w1", "w3"):
+                    lay[name + "_smooth"] = smooth_factors(HIDDEN, gen)
+            else:
+                lay = {name: Linear(K, N, g, gen) for name, (K, N) in LAYER_SHAPES.items()}
             lay["attn_norm"] = (1 + 0.1 * torch.randn(HIDDEN, generator=gen, device="cuda")).half()
             lay["ffn_norm"] = (1 + 0.1 * torch.randn(HIDDEN, generator=gen, device="cuda")).half()
             self.layers.append(lay)
@@ -69,6 +89,9 @@ class DecodeStack:
         self.xs = torch.empty((T, FFN // 64 + 1), device=dev, dtype=torch.float32)
         self.o_in = torch.empty((T, Q_DIM), device=dev, dtype=torch.float16)
         self.act = torch.empty((T, FFN), device=dev, dtype=torch.float16)
+        if awq:
+            self.gate = torch.empty((T, FFN), device=dev, dtype=torch.float16)
+            self.up = torch.empty((T, FFN), device=dev, dtype=torch.float16)
         lib = ops.lib()
         ops.check(lib.fa_workspace_reserve(max(T, 16), 19456, FFN, g, ops._stream()))
 
@@ -76,6 +99,71 @@ class DecodeStack:
     def linear(self, lay, name, x, out):
         L = lay[name]
         ops.w8a8_gemm(L.W, L.scale, x, L.g, out=out)
+
+    def run_stack_awq(self):
+        """The calibrated (AWQ) layout, five launches per layer:
+
+            qkv   fa_w8a8_gemm_rms       h' = h + down_prev; attention_norm(h') * smooth_qkv
+            o     fa_w8a8_gemm           the q slice of qkv's output
+            w1    fa_w8a8_gemm_rms       h'' = h' + o; ffn_norm(h'') * smooth_w1 -> gate
+            w3    fa_w8a8_gemm_rms       ffn_norm(h'') * smooth_w3 -> up
+            down  fa_w8a8_gemm_silu_mul  silu(gate) * up
+
+        (dual_ar_engine.cc:576-648 with each weight's QuantMeta, :253-275.)"""
+        assert self.awq
+        g, T = self.g, self.T
+        l_ = ops.lib()
+        s = ops._stream()
+        cur, nxt = self.h, self.h_alt
+        if T == 1:
+            o_in = self.y["qkv"]
+        for li, lay in enumerate(self.layers):
+            L = lay["qkv"]
+            resid = None if li == 0 else self.y["down"].data_ptr()
+            ops.check(l_.fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), g, None,
+                                          lay["qkv_smooth"].data_ptr(), cur.data_ptr(), resid,
+                                          None if li == 0 else nxt.data_ptr(),
+                                          lay["attn_norm"].data_ptr(), 1e-6,
+                                          self.y["qkv"].data_ptr(), L.N, T, L.K, s))
+            if li != 0:
+                cur, nxt = nxt, cur
+            if T != 1:
+                self.o_in.copy_(self.y["qkv"][:, :Q_DIM])
+                o_in = self.o_in
+            L = lay["o"]
+            ops.check(l_.fa_w8a8_gemm(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                      o_in.data_ptr(), self.y["o"].data_ptr(), L.N, T, L.K, s))
+            L = lay["w1"]
+            ops.check(l_.fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), g, None,
+                                          lay["w1_smooth"].data_ptr(), cur.data_ptr(),
+                                          self.y["o"].data_ptr(), nxt.data_ptr(),
+                                          lay["ffn_norm"].data_ptr(), 1e-6, self.gate.data_ptr(),
+                                          L.N, T, L.K, s))
+            cur, nxt = nxt, cur
+            L = lay["w3"]
+            ops.check(l_.fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), g, None,
+                                          lay["w3_smooth"].data_ptr(), cur.data_ptr(), None, None,
+                                          lay["ffn_norm"].data_ptr(), 1e-6, self.up.data_ptr(),
+                                          L.N, T, L.K, s))
+            L = lay["down"]
+            ops.check(l_.fa_w8a8_gemm_silu_mul(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                               self.gate.data_ptr(), self.up.data_ptr(),
+                                               self.y["down"].data_ptr(), L.N, T, L.K, s))
+        ops.check(l_.fa_residual_add(cur.data_ptr(), self.y["down"].data_ptr(), T * HIDDEN, s))
+        if cur is not self.h:
+            self.h.copy_(cur)
+
+    def awq_stack_bytes(self):
+        """Algorithmic bytes of one run_stack_awq pass: int8 W + fp16 scales,
+        the three smooth_inv vectors, gamma twice, and each linear's fp16
+        activations in and out (silu_mul reads gate and up)."""
+        tot = 0
+        for lay in self.layers:
+            for name in ("qkv", "o", "w1", "w3", "down"):
+                L = lay[name]
+                tot += L.algo_bytes + 2 * self.T * (L.K + L.N)
+            tot += 3 * 2 * HIDDEN + 2 * 2 * HIDDEN + 2 * self.T * FFN
+        return tot
 
     def run_linears(self, layer_ids=None):
         """configs[1]-style work: the four projections of each layer through
@@ -169,11 +257,18 @@ class DecodeStack:
         self.chain = ops.Chain(steps, self.g)
         return self.chain
 
-    def run_chain(self):
-        """run_stack's result through one chain launch (+ the last residual add)."""
+    def run_chain(self, check=True):
+        """run_stack's result through one chain launch (+ the last residual add).
+        check: wait for the launch and raise if a step's bounded wait gave up
+        (the outputs are then incomplete); callers timing back-to-back runs
+        pass False and check chain.status() themselves afterwards."""
         if getattr(self, "chain", None) is None:
             self.build_chain()
         self.chain.run()
+        if check:
+            rc = self.chain.status()
+            if rc != 0:
+                raise ops.FaError(rc, "decode chain: a step's wait gave up; outputs incomplete")
         cur = self._chain_out
         l_ = ops.lib()
         ops.check(l_.fa_residual_add(cur.data_ptr(), self.y["down"].data_ptr(), HIDDEN,

@@ -10,7 +10,7 @@ import sys
 
 import torch
 
-from ._lib import ChainStep, check, lib
+from ._lib import ChainStep, FaError, check, lib
 
 
 def _stream():

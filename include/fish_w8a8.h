@@ -19,6 +19,7 @@
 #ifndef FISH_W8A8_H
 #define FISH_W8A8_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
