@@ -17,6 +17,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -226,6 +227,97 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
                                            ws->xq, ws->xs, nullptr, N, K, g, G, s));
     return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             s);
+}
+
+// ------------------------------------------------- no-alloc variant ----
+//
+// fa_w8a8_gemm_noalloc: fa_w8a8_gemm with its scratch (x_q, x_scale and the
+// prefill scale tables) carved from one file-scope device array instead of
+// the grow-only per-thread workspace, so the call never allocates.  Each
+// device holds its own copy of the array; host code must use the address
+// hipGetSymbolAddress reports for the current device, never the symbol.
+}  // extern "C"
+
+namespace {
+
+constexpr size_t kNoallocBytes = (size_t)FA_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up once per device).
+int scratch_for_current_device(const char* fn, unsigned char** out) {
+    int dev = 0;
+    FA_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(FA_ERR_INVALID_ARG, "%s: device %d", fn, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        FA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(FA_ERR_HIP, "%s: no device address for the scratch array", fn);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+    return FA_OK;
+}
+
+size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+size_t fa_noalloc_scratch_bytes(int M, int N, int K, int group_size) {
+    if (M < 0 || N < 0 || K <= 0) return (size_t)-1;
+    const int g = eff_group(K, group_size);
+    const size_t G = (size_t)((K + g - 1) / g);
+    return round256((size_t)N * (size_t)K) + round256((size_t)N * G * sizeof(float)) +
+           round256(fa::gemm_pipe_tables_bytes(M, N, (int)G));
+}
+
+int fa_w8a8_gemm_noalloc(const int8_t* W, const uint16_t* w_scale, int group_size,
+                         const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* X,
+                         uint16_t* Y, int M, int N, int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_noalloc";
+    g_err.clear();
+    int rc = check_dims(fn, M, N, K);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return FA_OK;
+    if (!W || !w_scale || !X || !Y) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (overlaps(Y, (size_t)N * M, X, (size_t)N * K))
+        return fail(FA_ERR_INVALID_ARG, "%s: Y overlaps X", fn);
+    hipStream_t s = (hipStream_t)stream;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W) && aligned16(X)) {
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true);
+        if (gp.kind == 1 || gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, X, act_scale, smooth_inv, Y,
+                                   nullptr, 0, 0, 0, 0, M, N, K, g, G, s));
+            return FA_OK;
+        }
+    }
+    // (one token on a path without in-kernel quantization needs scratch too)
+    const size_t xq_bytes = round256((size_t)N * (size_t)K);
+    const size_t xs_bytes = round256((size_t)N * (size_t)G * sizeof(float));
+    const size_t need = fa_noalloc_scratch_bytes(M, N, K, group_size);
+    if (need > kNoallocBytes)
+        return fail(FA_ERR_INVALID_ARG,
+                    "%s: M=%d N=%d K=%d needs %zu B of scratch, above the %zu B maximum", fn, M, N,
+                    K, need, kNoallocBytes);
+    unsigned char* base = nullptr;
+    rc = scratch_for_current_device(fn, &base);
+    if (rc) return rc;
+    int8_t* xq = reinterpret_cast<int8_t*>(base);
+    float* xs = reinterpret_cast<float*>(base + xq_bytes);
+    float* tables = reinterpret_cast<float*>(base + xq_bytes + xs_bytes);
+    // every byte the kernels read is written first: nothing to clear
+    FA_HIP(fa::launch_quantize_activations(X, nullptr, fa::Prologue::kPlain, act_scale, smooth_inv,
+                                           xq, xs, nullptr, N, K, g, G, s));
+    return linear_quantized(fn, W, w_scale, g, G, xq, xs, Y, nullptr, 0, 0, 0, 0, M, N, K, s,
+                            tables);
 }
 
 int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,

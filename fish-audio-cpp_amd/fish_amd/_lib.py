@@ -13,6 +13,7 @@ FA_ERR_HIP = 2
 FA_ERR_IO = 3
 FA_ERR_FORMAT = 4
 FA_ERR_NOT_FOUND = 5
+FA_NOALLOC_SCRATCH_BYTES = 32 << 20   # include/fish_w8a8.h
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -68,6 +69,8 @@ SIGNATURES = {
     "fa_last_error": (ctypes.c_char_p, []),
     "fa_version": (ctypes.c_char_p, []),
     "fa_w8a8_gemm": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_w8a8_gemm_noalloc": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _p]),
+    "fa_noalloc_scratch_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
     "fa_w8a8_gemm_rms": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _f, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_silu_mul": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_gemm_fp16": (_i, [_p, _p, _p, _i, _i, _i, _p]),

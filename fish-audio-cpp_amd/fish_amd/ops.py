@@ -49,6 +49,19 @@ def w8a8_gemm(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=No
     return Y
 
 
+def w8a8_gemm_noalloc(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=None):
+    """fa_w8a8_gemm_noalloc: w8a8_gemm with its scratch in the library's
+    static per-device array (no device allocation inside the call)."""
+    _need(W, torch.int8, "W"); _need(w_scale, torch.float16, "w_scale"); _need(X, torch.float16, "X")
+    _need(act_scale, torch.float16, "act_scale"); _need(smooth_inv, torch.float16, "smooth_inv")
+    M, K = W.shape
+    N = X.shape[0]
+    Y = out if out is not None else torch.empty((N, M), dtype=torch.float16, device=X.device)
+    check(lib().fa_w8a8_gemm_noalloc(_ptr(W), _ptr(w_scale), group_size, _ptr(act_scale),
+                                     _ptr(smooth_inv), _ptr(X), _ptr(Y), M, N, K, _stream()))
+    return Y
+
+
 def w8a8_gemm_rms(W, w_scale, x, gamma, eps, group_size, resid=None, h_out=None,
                   act_scale=None, smooth_inv=None, out=None):
     """RMSNorm (after an optional residual add written to h_out) + linear."""

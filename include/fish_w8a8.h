@@ -54,6 +54,26 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
                  const uint16_t* act_scale, const uint16_t* smooth_inv,
                  const uint16_t* X, uint16_t* Y, int M, int N, int K, void* stream);
 
+/* Scratch maximum of fa_w8a8_gemm_noalloc, per device (32 MiB). */
+#define FA_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference: fa_w8a8_gemm for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * fa_w8a8_gemm, bit for bit; it never calls hipMalloc / hipFree.  Its scratch
+ * (x_q, x_scale and the prefill scale tables, fa_noalloc_scratch_bytes()
+ * bytes) lives in one statically sized device array of
+ * FA_NOALLOC_SCRATCH_BYTES per device, held until the process ends; shapes
+ * needing more fail with FA_ERR_INVALID_ARG (one token on aligned buffers
+ * needs none).  Every call on a device shares that device's array: calls
+ * that overlap in time on one device (two streams, two threads) race. */
+int fa_w8a8_gemm_noalloc(const int8_t* W, const uint16_t* w_scale, int group_size,
+                         const uint16_t* act_scale, const uint16_t* smooth_inv,
+                         const uint16_t* X, uint16_t* Y, int M, int N, int K, void* stream);
+/* Scratch bytes fa_w8a8_gemm_noalloc uses for this shape when it quantizes
+ * in a separate launch (an upper bound; (size_t)-1 for bad sizes). */
+size_t fa_noalloc_scratch_bytes(int M, int N, int K, int group_size);
+
 /* The FP16 weight path of DualAREngine::quantized_gemm
  * (dual_ar_engine.cc:338-341): gemm_fp16 (dac_engine.cc:19-32), i.e.
  * cublasGemmEx with fp16 W [M, K], fp16 X [N, K], fp16 Y (col-major [M, N],

@@ -1,0 +1,63 @@
+"""fa_w8a8_gemm_noalloc (scratch in a static per-device array, no allocation
+in the call) against fa_w8a8_gemm, bit for bit, on consecutive calls whose
+second input is smaller (the array keeps the first call's contents), plus
+the size limit."""
+import numpy as np
+import pytest
+import torch
+
+from fish_amd import _lib, ops, synth
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.array(a, copy=True, order="C")).cuda()
+
+
+def run_pair(N, M, K, g, seed, act=None, sm=None):
+    q, s = ref.quantize_weights(synth.weights_f16(M, K, seed=seed), g)
+    x = dev(synth.activations_f16(N, K, seed=seed + 1))
+    Wd, Sd = dev(q), dev(s)
+    a = ops.w8a8_gemm(Wd, Sd, x, g, act_scale=act, smooth_inv=sm)
+    b = ops.w8a8_gemm_noalloc(Wd, Sd, x, g, act_scale=act, smooth_inv=sm)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (N, M, K, g)
+    return b
+
+
+@pytest.mark.parametrize("first,second", [
+    ((2048, 2560, 9728, 256), (512, 6144, 2560, 256)),   # prefill tile kernel, then smaller
+    ((64, 512, 2560, 64), (8, 256, 2560, 64)),           # tile kernel, then the MFMA GEMV
+    ((8, 2560, 4096, 64), (1, 2560, 4096, 256)),         # GEMV, then one token (no scratch)
+    ((300, 260, 512, 256), (3, 40, 100, 48)),            # ragged tiles, then the generic kernel
+])
+def test_noalloc_matches_entry_point(first, second):
+    assert _lib.lib().fa_noalloc_scratch_bytes(*first) <= _lib.FA_NOALLOC_SCRATCH_BYTES
+    run_pair(*first, seed=1)
+    run_pair(*second, seed=2)
+
+
+def test_noalloc_static_and_smooth_companions():
+    K, g = 2560, 64
+    G = K // g
+    act = dev(np.full(G, 0.05, np.float16))
+    sm = dev(synth.gamma_f16(K, seed=3))
+    run_pair(16, 1024, K, g, seed=4, act=act, sm=sm)
+    run_pair(4, 512, K, g, seed=5, sm=sm)
+
+
+def test_noalloc_rejects_oversized_shape():
+    # 8192 tokens x K 9728 codes alone exceed the 32 MiB array
+    N, M, K, g = 8192, 256, 9728, 256
+    assert _lib.lib().fa_noalloc_scratch_bytes(M, N, K, g) > _lib.FA_NOALLOC_SCRATCH_BYTES
+    W = torch.zeros((M, K), dtype=torch.int8, device="cuda")
+    S = torch.ones((M, K // g), dtype=torch.float16, device="cuda")
+    X = torch.zeros((N, K), dtype=torch.float16, device="cuda")
+    with pytest.raises(_lib.FaError) as e:
+        ops.w8a8_gemm_noalloc(W, S, X, g)
+    assert e.value.code == _lib.FA_ERR_INVALID_ARG
+    assert "maximum" in str(e.value)
+    # the library still works afterwards
+    run_pair(4, 64, 512, 64, seed=6)
