@@ -43,6 +43,8 @@ def cpu_baseline(stack, torch, budget_s):
     linears at M=1 g256; median over repetitions within budget_s."""
     from oracle import ref
     from fish_amd.synth import LAYER_SHAPES
+    march = ref.use_baseline_build()
+    model = ref.host_cpu()[0]
     lay = stack.layers[0]
     host = {}
     nbytes = 0
@@ -67,6 +69,7 @@ def cpu_baseline(stack, torch, budget_s):
     med = statistics.median(times)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
+            "cpu_model": model, "build": "gcc -O3 -fopenmp -march=%s" % march,
             "sample": "one layer's 4 linears (qkv/o/gate_up/down) at M=1 g256, "
                       "%d reps, median %.2f ms" % (len(times), med * 1e3)}
 
@@ -141,12 +144,16 @@ def main():
         # The gate_up GEMV, then a plain 64 MiB device copy whose known byte
         # count calibrates the FETCH_SIZE / WRITE_SIZE counters.
         r = roofline_gate_up(torch, ops, st, LAYER_SHAPES)
+        del st
+        torch.cuda.empty_cache()
+        rp = roofline_prefill(torch, ops)
         a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
         b = torch.empty_like(a)
         for _ in range(3):
             b.copy_(a)
         torch.cuda.synchronize()
-        print(json.dumps({"roofline": r, "calibration_copy_bytes": 64 << 20}), flush=True)
+        print(json.dumps({"roofline": r, "roofline_prefill": rp,
+                          "calibration_copy_bytes": 64 << 20}), flush=True)
         return
 
     # ---- headline: configs[1] linears, graph-replayed --------------------
@@ -167,12 +174,16 @@ def main():
     value = step_bytes / (dt / args.steps) / 1e9
 
     roofline = roofline_gate_up(torch, ops, st, LAYER_SHAPES)
+    roofline_pf = None
 
     secondary = {}
     if not args.no_secondary:
         secondary = run_secondary(torch, ops, st, args)
 
     cpu = cpu_baseline(st, torch, args.cpu_budget)
+    del st
+    torch.cuda.empty_cache()
+    roofline_pf = roofline_prefill(torch, ops)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -185,6 +196,7 @@ def main():
                    "tokens": 1, "group_size": 256, "layers_per_step": args.layers,
                    "bytes_per_step": step_bytes, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
+        "roofline_prefill": roofline_pf,
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
@@ -218,30 +230,72 @@ def graph_us_per_call(torch, calls, reps=10, rounds=5):
     return statistics.median(per)
 
 
+def _traffic(key):
+    """HBM bytes per launch of `key` from the calibrated rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs committed under profiles/ (or None)."""
+    tpath = os.path.join(REPO, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        rec = json.load(open(tpath)).get(key)
+        if rec:
+            return rec["bytes_per_launch"]
+    return None
+
+
+GATE_UP_QX_KEY = "gemv_dot_kernel QX gate_up K=2560 N=19456 m1 g256"
+PREFILL_KEY = "gemm_tile_kernel gate_up K=2560 N=19456 M=2048 g256"
+
+
 def roofline_gate_up(torch, ops, st, LAYER_SHAPES):
-    """Dominant kernel of the headline: the gate_up GEMV (gemv_dot_kernel,
-    K=2560 N=19456, one token, g256), one launch per layer's weights so every
-    launch streams its 50 MB from HBM.  x is quantized once outside."""
-    xq, xs = ops.quantize_activations(st.x_in["gate_up"], 256)
+    """Dominant kernel of the headline: the gate_up linear exactly as the
+    headline runs it -- fa_w8a8_gemm at one token, i.e. gemv_dot_kernel with
+    in-kernel activation quantization (K=2560 N=19456, g256) -- one launch
+    per layer's weights so every launch streams its 50 MB from HBM, timed
+    with HIP events on the stream the launches go to (torch's current
+    stream).  Algorithmic bytes per launch: int8 W + fp16 scales + fp16 x
+    in + fp16 y out."""
+    x = st.x_in["gate_up"]
     out = st.y["gate_up"]
-    calls = [(lambda L=lay["gate_up"]: ops.w8a8_gemm_quantized(L.W, L.scale, 256, xq, xs, out=out))
+    calls = [(lambda L=lay["gate_up"]: ops.w8a8_gemm(L.W, L.scale, x, 256, out=out))
              for lay in st.layers]
     us = graph_us_per_call(torch, calls)
     K, N = LAYER_SHAPES["gate_up"]
     kbytes = st.layers[0]["gate_up"].algo_bytes + 2 * (K + N)
     achieved = kbytes / (us * 1e-6) / 1e9
-    # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    # (calibrated against a known-size copy), committed under profiles/
-    traffic = None
-    tpath = os.path.join(REPO, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        rec = json.load(open(tpath)).get("gemv_dot_kernel gate_up K=2560 N=19456 m1 g256")
-        if rec:
-            traffic = rec["bytes_per_launch"]
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "gemv_dot_kernel (gate_up, K=2560 N=19456, 1 token, g256)",
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(GATE_UP_QX_KEY),
+            "kernel": "gemv_dot_kernel, in-kernel quantization (fa_w8a8_gemm: gate_up, "
+                      "K=2560 N=19456, 1 token, g256)",
             "avg_launch_us": round(us, 3), "bytes_per_launch": kbytes}
+
+
+def roofline_prefill(torch, ops):
+    """Dominant kernel of the metric's prefill half: the gate_up GEMM at
+    2048 tokens, g256, through fa_w8a8_gemm_quantized
+    (gemm_tile_kernel; the call also runs the small scale-table launch,
+    which the timing includes).  Algorithmic work per call: 2*M*N*K int8
+    ops.  Random operands (the matrix units' clock depends on the data)."""
+    from fish_amd.synth import LAYER_SHAPES
+    K, N = LAYER_SHAPES["gate_up"]
+    M, g = 2048, 256
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+    W, S = ops.quantize_weights_groupwise(w, g)
+    del w
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    xq, xs = ops.quantize_activations(x, g)
+    y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+    us = graph_us_per_call(torch, [lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=y)] * 8,
+                           reps=5)
+    o = 2.0 * M * N * K
+    tops = o / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+            "traffic": _traffic(PREFILL_KEY),
+            "kernel": "gemm_tile_kernel (gate_up, K=2560 N=19456, 2048 tokens, g256), "
+                      "+ scale-table launch",
+            "avg_launch_us": round(us, 3), "ops_per_launch": o}
 
 
 def run_secondary(torch, ops, st, args):
@@ -296,6 +350,23 @@ def run_secondary(torch, ops, st, args):
     out["cfg4_awq_stack_g256_m1"] = {"step_ms": round(t * 1e3, 4),
                                      "GB/s": round(sa.awq_stack_bytes() / t / 1e9, 1)}
     del sa, g_awq
+    torch.cuda.empty_cache()
+    # the fast (codebook) decoder: 4 layers + int8 head (4096 x 2560), 10
+    # passes per frame over the same ~0.4 GB of weights
+    from fish_amd.decode_stack import FastDecoder, NUM_CODEBOOKS
+    fd = FastDecoder(g=256, seed=11)
+    g_fd = fd.capture(lambda: fd.run_frame())
+    for _ in range(2):
+        g_fd.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_fd.replay()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    out["fast_decoder_frame_g256"] = {"frame_ms": round(t * 1e3, 4), "passes": NUM_CODEBOOKS,
+                                      "GB/s": round(NUM_CODEBOOKS * fd.pass_bytes() / t / 1e9, 1)}
+    del fd, g_fd
     torch.cuda.empty_cache()
     # configs[1] per-linear GEMV time (graph of one launch per layer, cold weights)
     for name, (K, N) in LAYER_SHAPES.items():

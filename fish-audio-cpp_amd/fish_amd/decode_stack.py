@@ -292,3 +292,45 @@ class DecodeStack:
             fn()
         torch.cuda.synchronize()
         return g
+
+
+CODEBOOK_SIZE = 4096
+NUM_CODEBOOKS = 10
+
+
+class FastDecoder(DecodeStack):
+    """The fast (codebook) decoder pass of a frame
+    (DualAREngine::fast_codebook_decode_device, dual_ar_engine.cc:772-845):
+    4 layers of the slow layer's shapes (dual_ar_config.h:21-31), then the
+    final RMSNorm and the int8 output head (codebook_size 4096 x 2560,
+    :836-838), run once per codebook -- 10 times per frame.  The layer
+    linears are DecodeStack's (four fused launches per layer); the head is
+    fa_w8a8_gemm_rms.  Attention, RoPE and the codebook embedding are out of
+    scope: each pass starts from the same synthetic hidden state."""
+
+    def __init__(self, g=256, seed=0, n_layers=4):
+        super().__init__(n_layers=n_layers, g=g, tokens=1, seed=seed)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(seed + 1000)
+        self.head = Linear(HIDDEN, CODEBOOK_SIZE, g, gen)
+        self.fast_norm = (1 + 0.1 * torch.randn(HIDDEN, generator=gen, device="cuda")).half()
+        self.logits = torch.empty((1, CODEBOOK_SIZE), device="cuda", dtype=torch.float16)
+
+    def run_pass(self):
+        """One codebook step: the 4-layer stack from h0, then the head."""
+        self.h.copy_(self.h0)
+        self.run_stack()
+        L = self.head
+        ops.check(ops.lib().fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), self.g, None,
+                                             None, self.h.data_ptr(), None, None,
+                                             self.fast_norm.data_ptr(), 1e-6,
+                                             self.logits.data_ptr(), L.N, 1, L.K, ops._stream()))
+
+    def run_frame(self):
+        for _ in range(NUM_CODEBOOKS):
+            self.run_pass()
+
+    def pass_bytes(self):
+        """Algorithmic bytes of one pass: the stack's plus the head's W,
+        scales, gamma and activations."""
+        return self.stack_bytes() + self.head.algo_bytes + 2 * (2 * HIDDEN + CODEBOOK_SIZE)

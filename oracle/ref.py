@@ -11,6 +11,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "liboracle_w8a8.so")
+LIB_V4_PATH = os.path.join(HERE, "_build", "liboracle_w8a8_v4.so")
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -46,17 +47,53 @@ _SIGS = {
 _LIB = None
 
 
-def lib():
+def host_cpu():
+    """(model name, has AVX-512 F/BW/CD/DQ/VL) of this host, from /proc/cpuinfo."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    v4 = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    return model, v4
+
+
+def use_baseline_build():
+    """For the CPU-baseline timing only: load the x86-64-v4 build when this
+    host has AVX-512 (call before any other oracle function).  Returns the
+    -march level in use."""
     global _LIB
+    if _LIB is not None:
+        return getattr(_LIB, "_march", "x86-64-v3")
+    if host_cpu()[1] and os.path.exists(LIB_V4_PATH):
+        _load(LIB_V4_PATH, "x86-64-v4")
+    else:
+        lib()
+    return _LIB._march
+
+
+def lib():
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError("oracle not built: run `make -C oracle`")
-        l = ctypes.CDLL(LIB_PATH)
-        for k, (r, a) in _SIGS.items():
-            fn = getattr(l, k)
-            fn.restype = r
-            fn.argtypes = a
-        _LIB = l
+        _load(LIB_PATH, "x86-64-v3")
+    return _LIB
+
+
+def _load(path, march):
+    global _LIB
+    l = ctypes.CDLL(path)
+    l._march = march
+    for k, (r, a) in _SIGS.items():
+        fn = getattr(l, k)
+        fn.restype = r
+        fn.argtypes = a
+    _LIB = l
     return _LIB
 
 

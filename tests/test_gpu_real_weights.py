@@ -200,3 +200,37 @@ def test_awq_decode_stack_bitexact(g, T, layers):
         xq, xs, _ = ref.silu_mul_quant(gate, up, g)
         h = ref.residual_add(h, lin("down", xq, xs))
     assert same(host(st.h), h)
+
+
+# ------------------------------------------------------- fast decoder ----
+
+def test_fast_decoder_pass_bitexact():
+    """One codebook pass of the fast decoder (dual_ar_engine.cc:794-838): the
+    4-layer stack at the slow layer's shapes, then RMSNorm + the int8 output
+    head (4096 x 2560, one token) -- hidden state and logits bit-identical to
+    the oracle's sequence; a second pass repeats the first exactly."""
+    from fish_amd.decode_stack import FastDecoder, Q_DIM
+    g = 256
+    fd = FastDecoder(g=g, seed=21)
+    fd.run_pass()
+    torch.cuda.synchronize()
+    h = host(fd.h0)
+    for lay in fd.layers:
+        def lin(name, xq, xs):
+            return ref.gemm_quantized(host(lay[name].W), host(lay[name].scale), g, xq, xs)
+        xq, xs, _ = ref.rms_norm_quant(h, host(lay["attn_norm"]), 1e-6, g)
+        y = lin("qkv", xq, xs)
+        xq, xs = ref.quantize_activations(np.ascontiguousarray(y[:, :Q_DIM]), g)
+        h = ref.residual_add(h, lin("o", xq, xs))
+        xq, xs, _ = ref.rms_norm_quant(h, host(lay["ffn_norm"]), 1e-6, g)
+        y = lin("gate_up", xq, xs)
+        xq, xs, _ = ref.silu_mul_quant(np.ascontiguousarray(y[:, 0::2]),
+                                       np.ascontiguousarray(y[:, 1::2]), g)
+        h = ref.residual_add(h, lin("down", xq, xs))
+    assert same(host(fd.h), h)
+    xq, xs, _ = ref.rms_norm_quant(h, host(fd.fast_norm), 1e-6, g)
+    rl = ref.gemm_quantized(host(fd.head.W), host(fd.head.scale), g, xq, xs)
+    first = host(fd.logits).copy()
+    assert same(first, rl)
+    fd.run_pass()
+    assert same(host(fd.logits), first)
