@@ -752,12 +752,12 @@ struct fa_chain {
     fa::ch::ChainStepDev* d_steps = nullptr;
     int* d_sync = nullptr;
     int* d_flags = nullptr;
-    int epoch = 0;
     fa::ChainPlan plan{};
 };
 
 static void chain_free(fa_chain* c) {
     if (!c) return;
+    if (c->plan.trace) (void)hipFree(c->plan.trace);
     if (c->d_steps) (void)hipFree(c->d_steps);
     if (c->d_sync) (void)hipFree(c->d_sync);
     if (c->d_flags) (void)hipFree(c->d_flags);
@@ -775,11 +775,10 @@ int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_
         return fail(FA_ERR_INVALID_ARG, "%s: group_size=%d (64, 128 or 256)", fn, group_size);
     const int g = group_size;
     const int lg = g == 64 ? 6 : g == 128 ? 7 : 8;
-    const int rows = fa::chain_rows_per_task();
     const int kmax = fa::chain_max_k();
     std::vector<fa::ch::ChainStepDev> h((size_t)n_steps);
-    int64_t total = 0;
     int kp_max = 16, g_pad = 4, kh = 0;
+    int64_t term_floats = 0;
     for (int i = 0; i < n_steps; ++i) {
         const fa_chain_step& c = steps[i];
         if (!c.w || !c.w_scale || !c.x || !c.y)
@@ -802,9 +801,14 @@ int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_
         if (c.prologue == 0 && (c.x2 || c.gamma || c.h_out))
             return fail(FA_ERR_INVALID_ARG, "%s: step %d: x2 / gamma / h_out need prologue 2", fn,
                         i);
+        const int G = (c.k + g - 1) / g;
+        if ((int64_t)c.m * G < 2)
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: fewer than two weight scales", fn, i);
+        if ((int64_t)c.m * c.k >= ((int64_t)1 << 31))
+            return fail(FA_ERR_INVALID_ARG, "%s: step %d: weight of 2^31 bytes or more", fn, i);
         if (!aligned16(c.w) || !aligned16(c.x) || (c.x2 && !aligned16(c.x2)) ||
             (c.gamma && !aligned16(c.gamma)) || (c.h_out && !aligned16(c.h_out)) ||
-            ((uintptr_t)c.y & 3) || ((uintptr_t)c.w_scale & 1))
+            ((uintptr_t)c.y & 1) || ((uintptr_t)c.w_scale & 3))
             return fail(FA_ERR_INVALID_ARG, "%s: step %d: misaligned pointer", fn, i);
         const size_t k = (size_t)c.k;
         const size_t ny = c.epilogue == 1 ? (size_t)c.m / 2 : (size_t)c.m;
@@ -825,25 +829,32 @@ int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_
         d.M = c.m;
         d.K = c.k;
         d.lg_g = lg;
-        d.G = (c.k + g - 1) / g;
+        d.G = G;
+        d.MG = (int64_t)c.m * G;
         d.passes = (c.k + 511) / 512;
-        d.nblocks = (c.m + rows - 1) / rows;
-        d.task0 = (int)total;
         d.pro = c.prologue;
         d.epi = c.epilogue;
         d.eps = c.eps;
-        total += d.nblocks;
-        if (total > (1 << 30)) return fail(FA_ERR_INVALID_ARG, "%s: too many rows", fn);
-        const int kp = (c.k + 15) & ~15;
-        kp_max = kp > kp_max ? kp : kp_max;
-        // scale slots the last (padding) pass reads
-        const int gp = (d.passes + fa::kChainRing - 1) / fa::kChainRing * fa::kChainRing * (512 / g);
-        g_pad = gp > g_pad ? gp : g_pad;
-        if (c.prologue == 2) kh = kp > kh ? kp : kh;
+        kp_max = c.k > kp_max ? c.k : kp_max;
+        g_pad = G > g_pad ? G : g_pad;
+        if (c.prologue == 2) kh = c.k > kh ? c.k : kh;
     }
-    g_pad = (g_pad + 3) & ~3;
-    const size_t lds = fa::chain_lds_bytes(kp_max, g_pad, kh);
-    if (lds > 64 * 1024) return fail(FA_ERR_INVALID_ARG, "%s: steps need %zu B of LDS", fn, lds);
+    const int cus = fa::chain_cus();
+    if (cus <= 0) return fail(FA_ERR_HIP, "%s: device query failed", fn);
+    for (const fa::ch::ChainStepDev& d : h) {
+        // a workgroup's term table: 2 rows per pair, at most ceil(pairs / cus) pairs
+        const int64_t pairs = ((int64_t)d.M + 1) / 2;
+        const int64_t tf = 2 * ((pairs + cus - 1) / cus) * d.G;
+        term_floats = tf > term_floats ? tf : term_floats;
+    }
+    if (term_floats > (1 << 20)) return fail(FA_ERR_INVALID_ARG, "%s: steps too large", fn);
+    const fa::ch::ChainLds l8 = fa::chain_lds(8, kp_max, kh, g_pad, (int)term_floats);
+    const int depth = fa::chain_depth_for(l8.total);
+    const fa::ch::ChainLds lay = fa::chain_lds(depth, kp_max, kh, g_pad, (int)term_floats);
+    if (lay.total > 160 * 1024)
+        return fail(FA_ERR_INVALID_ARG, "%s: steps need %d B of LDS", fn, lay.total);
+    const int grid = fa::chain_grid(lg, depth, (size_t)lay.total);
+    if (grid < cus) return fail(FA_ERR_HIP, "%s: occupancy query failed (grid %d)", fn, grid);
     fa_chain* c = new fa_chain();
     if (hipGetDevice(&c->dev) != hipSuccess ||
         hipMalloc((void**)&c->d_steps, h.size() * sizeof(h[0])) != hipSuccess ||
@@ -856,26 +867,22 @@ int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_
         chain_free(c);
         return fail(FA_ERR_HIP, "%s: device allocation / upload failed", fn);
     }
-    int coop = 0;
-    const int grid = fa::chain_grid(lg, lds);
-    if (grid <= 0 ||
-        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->dev) != hipSuccess ||
-        !coop) {
-        chain_free(c);
-        return fail(FA_ERR_HIP, "%s: occupancy query failed or no cooperative launch", fn);
-    }
     c->plan.steps = c->d_steps;
     c->plan.sync = c->d_sync;
     c->plan.flags = c->d_flags;
     c->plan.nsteps = n_steps;
-    c->plan.total = (int)total;
     c->plan.lg = lg;
-    c->plan.grid = grid < total ? grid : (int)total;
+    c->plan.grid = cus;   // one workgroup per CU (the term tables are sized for it)
     c->plan.spin_limit = 1 << 21;
-    c->plan.kp_max = kp_max;
-    c->plan.g_pad = g_pad;
-    c->plan.kh = kh;
-    c->plan.lds = lds;
+    c->plan.depth = depth;
+    c->plan.lay = lay;
+    c->plan.trace = nullptr;
+#ifdef FA_CHAIN_TRACE
+    if (hipMalloc((void**)&c->plan.trace, (size_t)(n_steps + 1) * cus * 8 * 8) != hipSuccess) {
+        chain_free(c);
+        return fail(FA_ERR_HIP, "%s: trace allocation failed", fn);
+    }
+#endif
     *out = c;
     return FA_OK;
 }
@@ -889,9 +896,6 @@ int fa_chain_run(fa_chain* chain, void* stream) {
     if (dev != chain->dev)
         return fail(FA_ERR_INVALID_ARG, "%s: chain lives on device %d, current is %d", fn,
                     chain->dev, dev);
-    // flags hold the epoch of the launch that set them: a new value per launch
-    chain->epoch = chain->epoch == 0x7fffffff ? 1 : chain->epoch + 1;
-    chain->plan.epoch = chain->epoch;
     FA_HIP(fa::launch_chain(chain->plan, (hipStream_t)stream));
     return FA_OK;
 }
@@ -915,6 +919,16 @@ int fa_chain_set_spin_limit(fa_chain* chain, int polls) {
     chain->plan.spin_limit = polls;
     return FA_OK;
 }
+
+#ifdef FA_CHAIN_TRACE
+// measurement builds only: copy the last run's per-step timestamps
+int fa_chain_trace(fa_chain* chain, void* host, size_t bytes) {
+    if (!chain || !chain->plan.trace) return FA_ERR_INVALID_ARG;
+    FA_HIP(hipDeviceSynchronize());
+    FA_HIP(hipMemcpy(host, chain->plan.trace, bytes, hipMemcpyDeviceToHost));
+    return FA_OK;
+}
+#endif
 
 int fa_chain_destroy(fa_chain* chain) {
     g_err.clear();

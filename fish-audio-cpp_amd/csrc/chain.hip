@@ -1,15 +1,15 @@
 // chain.hip -- a decode step's W8A8 linears (one token) as ONE persistent
-// launch: the device orders the linears, and the weight stream of linear
-// s + 1 is already in flight while linear s finishes.
+// launch: the device orders the linears, and every workgroup keeps the next
+// linear's weights streaming into LDS while the previous one finishes.
 //
 // Replaces the per-linear launch sequence of DualAREngine::decode_step
 // (src/engine/dual_ar_engine.cc:576-648: rms_norm -> quantize -> int8 GEMV ->
 // ... per projection) for the int8 projections; each step computes exactly
-// what the fused N == 1 GEMV kernels compute (gemv_kernels.h, R = 2):
+// what the fused N == 1 GEMV kernels compute (gemv_kernels.h):
 //   prologue 0: x -> per-group dynamic int8 codes (int8_gemm.cu:147-211);
 //   prologue 2: h = fp16(x + x2) (residual_add, ffn_activations.cu:41-45),
-//               rms_norm(h, gamma) (rms_norm.cu:10-58), then the quantizer; the
-//               step's first row block writes h to h_out;
+//               rms_norm(h, gamma) (rms_norm.cu:10-58), then the quantizer;
+//               workgroup 0 writes h to h_out;
 //   epilogue 0: y[row] = fp16 of the group-ordered fp32 sum (int8_gemm.cu:
 //               213-234, acc = fma(float(P_g) * ws, xs, acc) over g in order);
 //   epilogue 1: rows 2i / 2i + 1 are the interleaved w1 / w3 rows of FFN
@@ -18,96 +18,120 @@
 // Every int32 group partial is exact and every fp32 operation happens in the
 // reference order, so each step's output is bit-identical to the oracle's.
 //
-// Work.  Step s has nblocks row blocks of ROWS rows; workgroup b owns blocks
-// b, b + grid, ... of every step.  Its work list -- (step, block, 512-byte
-// pass) in order -- is walked by two uniform cursors: a load cursor KD passes
-// ahead fills a register ring of 16-byte weight loads, a consume cursor
-// drains it.  The weight loads never depend on activations, so the ring runs
-// ahead across block and step boundaries: the next step's weights are in
-// flight while the workgroup waits for the previous step to finish.
+// Work.  One workgroup per CU: 8 streaming waves and one control wave.  Step
+// s's rows, in pairs, are split evenly over the workgroups (contiguous pair
+// ranges); a workgroup's (pair, 512-byte pass) items are split evenly over
+// its streaming waves (contiguous item ranges, which may cut a row between
+// two waves).  An item is one pass of a row pair: each of the 64 lanes
+// multiplies 16 weight bytes with 16 activation codes (4 v_dot4), lanes of
+// one K-group add their partials with DPP, and the group's leader lane
+// writes the exact term float(P_g) * ws to an LDS term table [row][group].
+// At the step's end the control wave runs each row's fp32 chain over the
+// terms in group order -- so splitting a row between waves changes nothing.
 //
-// Ordering.  When the consumer reaches its first block of step s it waits
-// until every block of step s - 1 is done (a per-step counter that each
-// workgroup bumps once, by its block count, after its last block of the
-// step), then forms the step's activation codes in LDS.  The grid is
-// launched cooperatively (all workgroups resident), so every awaited block
-// has a running owner.  Each wait is bounded: past `spin_limit` polls the
-// workgroup raises the error word and every waiting workgroup gives up.
+// Ring.  Each streaming wave owns an LDS ring of DEPTH slots.  A slot holds
+// one item's weights (64 lanes x 16 bytes) and the fp16 scale pair of each
+// lane's group (64 x 4 bytes), both loaded straight into LDS by
+// global_load_lds (no registers held).  The wave's item list runs across
+// steps, and the ring is refilled DEPTH items ahead of the consumer as soon
+// as a slot is read, so while the workgroup waits for step s - 1 to finish
+// everywhere, DEPTH items of step s are already landing (8 x DEPTH KB per CU).
+// The streaming waves issue no other global memory operation: every wait
+// is `s_waitcnt vmcnt(2 * (DEPTH - 1))`, exactly one item old.
 //
-// Signals.  A workgroup adds its block count to the step's counter once,
-// after its last block of the step; the one whose add completes the count
-// writes the launch's epoch into the step's flag, one copy per XCD (128 bytes
-// apart), and waiters poll the copy of their own XCD -- so no line is hit by
-// every workgroup at once.  The epoch changes every launch, so flags are
-// never cleared.
+// Control wave.  Between steps (three workgroup barriers): it turns the
+// terms of step s - 1 into outputs and stores them (agent-scope sc1 stores),
+// waits for its stores, counts the workgroup into the step's counter (8
+// copies, one per XCD, 128 bytes apart; adds whose result is not awaited),
+// polls its XCD's copy until every workgroup is counted, and loads step s's
+// inputs into LDS with sc1 direct-to-LDS loads; then all waves form the
+// step's int8 codes in LDS (the prologue), and the streaming waves go on.
+// Each wait is bounded: past `spin_limit` polls the wave raises the error
+// word and every workgroup leaves.  The launch is an ordinary one whose grid
+// is the number of workgroups the device holds at once, so every awaited
+// workgroup is running (a missing one would only make the bounded waits
+// give up).
 //
-// Memory.  Outputs (y, h_out) are written and activation inputs read with
-// agent-scope accesses (sc1: coherent across the XCDs' L2s, no whole-cache
-// write-back or invalidation), and a writer waits for its stores to complete
-// (s_waitcnt vmcnt(0)) before its counter add.
-//
-// sync[s]: finished blocks of step s (0 .. nsteps - 1); sync[nsteps]: error
-// word; both zero before a launch.  flags[(s * 8 + x) * 32]: step s done, for
-// XCD x.
+// flags[(s * 8 + x) * 32]: workgroups done with step s, copy x; sync[nsteps]:
+// error word.  A small kernel zeroes both before each launch.
 #include "common.h"
 #include "chain.h"
 
 namespace fa {
 namespace {
 
+using ch::ChainLds;
 using ch::ChainStepDev;
 
-constexpr int R = 2;              // rows per wave
-constexpr int RL = 64 / R;        // lanes per row
-constexpr int PB = RL * 16;       // bytes of a row per pass
-constexpr int KD = kChainRing;    // passes in flight per wave
+#ifdef FA_CHAIN_TRACE
+constexpr bool kTrace = true;    // measurement build: per-step timestamps
+#else
+constexpr bool kTrace = false;
+#endif
+#ifdef FA_CHAIN_SIG_FLAGS
+constexpr bool kSigCopies = false;  // measurement builds: one counter, last adder raises flags
+#else
+constexpr bool kSigCopies = true;   // 8 counter copies, adds not awaited (measured faster)
+#endif
+#ifdef FA_CHAIN_SLEEP
+constexpr int kSleep = FA_CHAIN_SLEEP;
+#else
+constexpr int kSleep = 1;
+#endif
+#ifdef FA_CHAIN_AB
+constexpr int kAb = FA_CHAIN_AB;    // measurement builds: 1 = no scale loads (wrong results)
+#else
+constexpr int kAb = 0;
+#endif
+#ifdef FA_CHAIN_PREFETCH
+constexpr bool kPrefetch = true;    // measurement builds: cache prefetch ahead of the ring
+#else
+constexpr bool kPrefetch = false;   // measured slower: the prefetched lines do not survive in L2
+#endif
 
-// Global-address-space loads: the ring selects between two row pointers,
-// which would otherwise leave generic pointers and flat loads (counted by
-// lgkmcnt as well, so every LDS wait would drain the ring).
-typedef __attribute__((address_space(1))) const v4i gv4i;
-typedef __attribute__((address_space(1))) const uint16_t gu16;
-__device__ __forceinline__ v4i ld16c(const int8_t* p) {
-    return *(gv4i*)(__builtin_bit_cast(uintptr_t, p));
-}
-__device__ __forceinline__ uint16_t ldu16g(const uint16_t* p) {
-    return *(gu16*)(__builtin_bit_cast(uintptr_t, p));
-}
+constexpr int NS = kChainWaves;          // streaming waves
+constexpr int NTS = NS * 64;             // streaming threads
+constexpr int NTH = NTS + 64;            // plus the control wave
+constexpr int PB = 512;                  // bytes of a row per item (32 lanes x 16)
+constexpr int kSlot = 1024 + 256;        // ring slot: weights, then scale pairs
+constexpr int XV = kChainMaxK / (NTS * 8);   // 8-value chunks per streaming thread
+static_assert(XV * NTS * 8 == kChainMaxK, "chunking");
 
-// Agent-scope (sc1) accesses: outputs and signals, coherent across the XCDs.
 typedef __attribute__((address_space(1))) uint32_t gu32;
 __device__ __forceinline__ gu32* g32(const void* p) {
     return (gu32*)(__builtin_bit_cast(uintptr_t, p));
 }
-__device__ __forceinline__ v4i ld16_coh(const uint16_t* p) {
-    gu32* q = g32(p);
-    v4i r;
-    r.x = (int)__hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.y = (int)__hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.z = (int)__hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.w = (int)__hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return r;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
 }
-// a step's activation input (written by an earlier step of this launch)
-__device__ __forceinline__ v4i ld16_act(const uint16_t* p) {
-#ifdef FA_CHAIN_X_CACHED
-    return ld16c(reinterpret_cast<const int8_t*>(p));
-#else
-    return ld16_coh(p);
-#endif
+
+// Direct-to-LDS loads: lane i's bytes land at lds + i * size (m0 = the
+// wave-uniform LDS base).
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
 }
-__device__ __forceinline__ void st16_coh(uint16_t* p, const v4i& v) {
-    gu32* q = g32(p);
-    __hip_atomic_store(q + 0, (uint32_t)v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 1, (uint32_t)v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 2, (uint32_t)v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 3, (uint32_t)v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
 }
+// ... agent-coherent (sc1): data written by other workgroups of this launch
+__device__ __forceinline__ void dma16_coh(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1"
+                 :: "v"(g), "s"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ void st2_coh(uint16_t* p, uint16_t v) {
     asm volatile("global_store_short %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
-// every store this wave issued has completed
-__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); }
+__device__ __forceinline__ void st16_coh(uint16_t* p, const v4i& v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
 
 // Max of a non-negative float over aligned blocks of 2^lgl lanes.
 __device__ __forceinline__ float lane_block_max(float m, int lgl) {
@@ -130,224 +154,372 @@ __device__ __forceinline__ int lane_group_sum(int p) {
     return p;
 }
 
-// One row block of a step, as the ring needs it (uniform values).
-struct Blk {
-    int s, blk, P;                // step, block, passes padded to a multiple of KD
+// The step fields a cursor needs (wave-uniform).
+struct StepC {
+    const int8_t* W;
+    const uint16_t* ws;
+    int M, K, G, lg, passes, mg2;
+};
+__device__ __forceinline__ StepC step_c(const ChainStepDev& st) {
+    StepC c;
+    c.W = st.W;
+    c.ws = st.w_scale;
+    c.M = st.M;
+    c.K = st.K;
+    c.G = st.G;
+    c.lg = st.lg_g;
+    c.passes = st.passes;
+    c.mg2 = (int)st.MG - 2;
+    return c;
+}
+
+__device__ __forceinline__ int ufirst(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// A wave's walk through its items: step s, pair pl (within the workgroup's
+// pairs pa + ...), pass; `rem` items of the step left.  All wave-uniform.
+struct Cursor {
+    int s, pa, pl, pass, rem;
+    StepC c;
 };
 
-// LG = g / 16 lanes per K-group (g = 64, 128 or 256), NWV waves per workgroup.
-template <int LG, int NWV>
-__global__ __launch_bounds__(NWV * 64) void chain_kernel(const ChainStepDev* __restrict__ steps,
-                                                         int nsteps, int* __restrict__ sync,
-                                                         int* __restrict__ flags, int epoch,
-                                                         int spin_limit, int kp_max, int g_pad,
-                                                         int kh) {
-    constexpr int NT = NWV * 64;
-    constexpr int GPP = RL / LG;            // groups per row per pass
-    constexpr int ROWS = NWV * R;           // rows per block
-    constexpr int XV = kChainMaxK / (NT * 8);          // activation chunks per thread
-    constexpr int XV2 = kChainMaxKPro / (NT * 8);      // ... with prologue 2
-    static_assert(XV * NT * 8 == kChainMaxK && XV2 * NT * 8 == kChainMaxKPro, "chunking");
-    extern __shared__ __align__(16) float lds[];
-    int8_t* xq_s = reinterpret_cast<int8_t*>(lds);                // [kp_max]
-    float* xs_s = lds + kp_max / 4;                               // [g_pad]
-    uint16_t* h_s = reinterpret_cast<uint16_t*>(xs_s + g_pad);    // [kh] (prologue 2)
-    float* red_s = reinterpret_cast<float*>(h_s + kh);            // [33]
-    int* ctl_s = reinterpret_cast<int*>(red_s + 34);              // [2]
-    uint16_t* y_s0 = reinterpret_cast<uint16_t*>(ctl_s + 2);      // [2][ROWS]
-
+// LG = g / 16 lanes per K-group (g = 64, 128 or 256); DEPTH ring slots; PF:
+// each item issue also touches the weight lines of the item DEPTH + PFD
+// ahead (cache prefetch); TR: per-step timestamps (measurement builds).
+template <int LG, int DEPTH, bool PF, bool TR>
+__global__ __launch_bounds__(NTH, 1) void chain_kernel(const ChainStepDev* __restrict__ steps,
+                                                      int nsteps, int* __restrict__ sync,
+                                                      int* __restrict__ flags,
+                                                      int spin_limit, ChainLds lay,
+                                                      unsigned long long* __restrict__ trace) {
+    constexpr int NOPS = (PF ? 3 : 2) - (kAb == 1 ? 1 : 0);   // global ops per item issue
+#ifdef FA_CHAIN_PFD
+    constexpr int PFD = FA_CHAIN_PFD;    // measurement builds: other prefetch distances
+#else
+    constexpr int PFD = 2 * DEPTH;       // prefetch distance beyond the ring
+#endif
+    extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = ufirst(tid >> 6);
     const int lane = tid & 63;
-    const int rsub = lane / RL;
-    const int li = lane % RL;
-    const int lane_k = li * 16;
+    const bool ctrl = wave == NS;
     const int b = blockIdx.x;
     const int grid = gridDim.x;
+    int8_t* const xq_s = reinterpret_cast<int8_t*>(smem + lay.xq);
+    float* const xs_s = reinterpret_cast<float*>(smem + lay.xs);
+    unsigned char* const stage = smem + lay.stage;       // inputs, then the step's terms
+    float* const terms = reinterpret_cast<float*>(stage);   // [group][row of the workgroup]
+    float* const red_s = reinterpret_cast<float*>(smem + lay.red);   // [33] + status
+    int* const ctl_s = reinterpret_cast<int*>(red_s + 34);
     int* const err = sync + nsteps;
     const v4i zero = {0, 0, 0, 0};
-
-    // this workgroup's first block at or after step s (s == nsteps: none)
-    auto first_from = [&](int s) {
-        while (s < nsteps && b >= steps[s].nblocks) ++s;
-        Blk r;
-        r.s = s;
-        r.blk = b;
-        r.P = s < nsteps ? (steps[s].passes + KD - 1) / KD * KD : KD;
-        return r;
-    };
-    auto next_of = [&](const Blk& c) {
-        if (c.blk + grid < steps[c.s].nblocks) {
-            Blk r = c;
-            r.blk += grid;
-            return r;
+    const int rsub = lane >> 5;              // row of the pair this lane reads
+    const int lk = (lane & 31) * 16;         // byte of the pass this lane reads
+    auto tr = [&](int s, int e) {
+        if constexpr (TR) {
+            if (ctrl && lane == 0)
+                trace[((size_t)s * grid + b) * 8 + e] = __builtin_amdgcn_s_memrealtime();
         }
-        return first_from(c.s + 1);
-    };
-    // Per-lane weight-row and scale-row pointers of a block (row clamped;
-    // past the end of the list: row 0 of step 0, never consumed).
-    struct RowPtr {
-        const int8_t* w;
-        const uint16_t* ws;
-        int K, lg_g;
-    };
-    auto row_ptr = [&](const Blk& c) {
-        const bool live = c.s < nsteps;
-        const ChainStepDev& st = steps[live ? c.s : 0];
-        const int row = (c.blk * NWV + wave) * R + rsub;
-        const int rowc = live ? (row < st.M ? row : st.M - 1) : 0;
-        RowPtr r;
-        r.w = st.W + (size_t)rowc * st.K;
-        r.ws = st.w_scale + (size_t)rowc * st.G;
-        r.K = st.K;
-        r.lg_g = st.lg_g;
-        return r;
     };
 
-    Blk cur = first_from(0);
-    if (cur.s >= nsteps) return;
-
-    v4i a[KD];
-    uint16_t sc[KD];
-    // pass p of a block: bytes past K (padding passes) re-read the row start
-    auto load = [&](int slot, const RowPtr& rp, int pass) {
-        const int k = pass * PB + lane_k;
-        const int kk = k < rp.K ? k : 0;
-        a[slot] = ld16c(rp.w + kk);
-        sc[slot] = ldu16g(rp.ws + (kk >> rp.lg_g));
+    // pairs [pa, pb) of a step with M rows owned by this workgroup
+    auto wg_pairs = [&](int M, int& pa, int& pb) {
+        const int64_t P = (M + 1) >> 1;
+        pa = (int)(P * b / grid);
+        pb = (int)(P * (b + 1) / grid);
     };
-    {
-        const RowPtr rp = row_ptr(cur);
-#pragma unroll
-        for (int q = 0; q < KD; ++q) load(q, rp, q);
+    // this wave's first item of step s: cursor fields
+    auto start = [&](Cursor& u, int s) {
+        u.s = s;
+        if (s >= nsteps) return;
+        u.c = step_c(steps[s]);
+        int pa, pb;
+        wg_pairs(u.c.M, pa, pb);
+        const int n = (pb - pa) * u.c.passes;
+        const int i0 = (int)((int64_t)n * wave / NS);
+        const int i1 = (int)((int64_t)n * (wave + 1) / NS);
+        u.pa = pa;
+        u.pl = i0 / u.c.passes;
+        u.pass = i0 - u.pl * u.c.passes;
+        u.rem = i1 - i0;
+    };
+    // next item (skipping steps where this wave has none)
+    auto advance = [&](Cursor& u) {
+        if (++u.pass == u.c.passes) {
+            u.pass = 0;
+            ++u.pl;
+        }
+        if (--u.rem == 0) {
+            start(u, u.s + 1);
+            while (u.s < nsteps && u.rem == 0) start(u, u.s + 1);
+        }
+    };
+    auto first = [&](Cursor& u) {
+        start(u, 0);
+        while (u.s < nsteps && u.rem == 0) start(u, u.s + 1);
+    };
+    // this lane's weight and scale-pair addresses of item u (rows past M
+    // read row M - 1; bytes past K read the row start: both never used)
+    auto item_addr = [&](const Cursor& u, const int8_t*& wp, const uint16_t*& sp) {
+        int row = 2 * (u.pa + u.pl) + rsub;
+        row = row < u.c.M ? row : u.c.M - 1;
+        int k = u.pass * PB + lk;
+        k = k < u.c.K ? k : 0;
+        wp = u.c.W + (uint32_t)(row * u.c.K + k);
+        int lo = (row * u.c.G + (k >> u.c.lg)) & ~1;
+        lo = lo < u.c.mg2 ? lo : u.c.mg2;
+        sp = u.c.ws + lo;
+    };
+
+    const uint32_t ring = lds_addr(smem) + (uint32_t)(ctrl ? 0 : wave) * DEPTH * kSlot;
+    const uint32_t junk = lds_addr(smem + lay.red) + 64 * 4;   // prefetch landing (256 B)
+    Cursor ld{}, pf{}, cs{};
+    auto issue = [&](int slot) {
+        const int8_t* wp = steps[0].W;
+        const uint16_t* sp = steps[0].w_scale;
+        if (ld.s < nsteps) {
+            item_addr(ld, wp, sp);
+            advance(ld);
+        }
+        // past the end of the list: re-read a valid address (keeps every
+        // wave's wait counts exact); those slots are never consumed
+        const uint32_t base = ufirst(ring + (uint32_t)slot * kSlot);
+        dma16(wp, base);
+        if constexpr (kAb != 1) dma4(sp, base + 1024);
+        if constexpr (PF) {
+            const int8_t* pw = steps[0].W;
+            const uint16_t* ps;
+            if (pf.s < nsteps) {
+                item_addr(pf, pw, ps);
+                advance(pf);
+            }
+            // every 64-byte line of the item, from 16 lanes
+            if ((lane & 3) == 0) dma4(pw, junk);
+        }
+    };
+    int slot = 0;
+    if (!ctrl) {
+        first(ld);
+        first(pf);
+        for (int q = 0; q < PFD; ++q)
+            if (pf.s < nsteps) advance(pf);
+#pragma unroll 1
+        for (int q = 0; q < DEPTH; ++q) issue(q);
     }
 
-    int done_here = 0;        // blocks of `prepared` finished by this workgroup
-    int fin = 0;              // blocks finished (parity picks the output staging half)
-    int prepared = -1;        // step whose activation codes are in LDS
-
-    auto signal = [&](int s) {
-        stores_done();
-        __syncthreads();
-        if (tid == 0) {
-            const int old = (int)__hip_atomic_fetch_add(g32(sync + s), (uint32_t)done_here,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            // every other owner's add (each after its own stores completed)
-            // is performed: the step is done
-            if (old + done_here == steps[s].nblocks) {
+    for (int s = 0; s <= nsteps; ++s) {
+        // ---- between steps s - 1 and s
+        __syncthreads();   // A: every term of step s - 1 is in LDS
+        tr(s, 0);
+        if (ctrl) {
+            int status = 0;
+            if (s > 0) {
+                // outputs of step s - 1 from its terms, in group order
+                const ChainStepDev& st = steps[s - 1];
+                int pa, pb;
+                wg_pairs(st.M, pa, pb);
+                const int np = pb - pa, G = st.G, nr = 2 * np;
+                if (st.epi == 1) {
+                    for (int pl = lane; pl < np; pl += 64) {
+                        float a0 = 0.0f, a1 = 0.0f;
+                        const float* t = terms + 2 * pl;
+                        int g = 0;
+                        for (; g + 4 <= G; g += 4) {
+                            float u0[4], u1[4];
 #pragma unroll
-                for (int x = 0; x < 8; ++x)
-                    __hip_atomic_store(g32(flags + (s * 8 + x) * 32), (uint32_t)epoch,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            for (int j = 0; j < 4; ++j) {
+                                u0[j] = t[(g + j) * nr];
+                                u1[j] = t[(g + j) * nr + 1];
+                            }
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                a0 = __builtin_fmaf(u0[j], xs_s[g + j], a0);
+                                a1 = __builtin_fmaf(u1[j], xs_s[g + j], a1);
+                            }
+                        }
+                        for (; g < G; ++g) {
+                            a0 = __builtin_fmaf(t[g * nr], xs_s[g], a0);
+                            a1 = __builtin_fmaf(t[g * nr + 1], xs_s[g], a1);
+                        }
+                        const uint16_t gh = f2h(a0), uh = f2h(a1);
+                        st2_coh(st.Y + pa + pl, f2h(h2f(f2h(silu_f(h2f(gh)))) * h2f(uh)));
+                    }
+                } else {
+                    for (int r = lane; r < nr; r += 64) {
+                        const int row = 2 * pa + r;
+                        float a = 0.0f;
+                        const float* t = terms + r;
+                        int g = 0;
+                        for (; g + 8 <= G; g += 8) {
+                            float u[8];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) u[j] = t[(g + j) * nr];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) a = __builtin_fmaf(u[j], xs_s[g + j], a);
+                        }
+                        for (; g < G; ++g) a = __builtin_fmaf(t[g * nr], xs_s[g], a);
+                        if (row < st.M) st2_coh(st.Y + row, f2h(a));
+                    }
+                }
+                wait_vm<0>();   // this wave's stores (outputs, h_out) are done
+                if constexpr (kSigCopies) {
+                    // count the workgroup into the step's 8 counter copies (one
+                    // per XCD); no returned value is awaited
+                    if (lane < 8)
+                        (void)__hip_atomic_fetch_add(g32(flags + ((s - 1) * 8 + lane) * 32), 1u,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else if (lane == 0) {
+                    // count the workgroup; the last one raises the step's 8
+                    // per-XCD flag lines
+                    const int old = (int)__hip_atomic_fetch_add(
+                        g32(sync + s - 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (old + 1 == grid) {
+#pragma unroll
+                        for (int x = 0; x < 8; ++x)
+                            __hip_atomic_store(g32(flags + ((s - 1) * 8 + x) * 32), (uint32_t)grid,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                tr(s, 1);
             }
-        }
-        done_here = 0;
-    };
-
-    for (;;) {
-        const ChainStepDev& st = steps[cur.s];
-        const int K = st.K, lg_g = st.lg_g, M = st.M;
-        // ---- a new step: signal the last one, wait for s - 1, prologue
-        if (cur.s != prepared) {
-            if (prepared >= 0) signal(prepared);
-            const int s = cur.s;
-            if (tid == 0) {
-                int status = 0;
+            if (s < nsteps) {
                 if (s > 0) {
-                    gu32* const flag = g32(flags + ((s - 1) * 8 + (b & 7)) * 32);
+                    // every workgroup has finished step s - 1
+                    gu32* const cnt = g32(flags + ((s - 1) * 8 + (b & 7)) * 32);
                     int polls = 0;
-                    while ((int)__hip_atomic_load(flag, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+                    while ((int)__hip_atomic_load(cnt, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) < grid) {
                         if (++polls > spin_limit ||
                             ((polls & 63) == 0 &&
-                             __hip_atomic_load(g32(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+                             __hip_atomic_load(g32(err), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))) {
                             status = 1;
-                            __hip_atomic_store(g32(err), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store(g32(err), 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
                             break;
                         }
-                        __builtin_amdgcn_s_sleep(2);
+                        __builtin_amdgcn_s_sleep(kSleep);
                     }
                 }
-                asm volatile("" : : : "memory");
-                ctl_s[1] = status;
+                tr(s, 2);
+                if (status == 0) {
+                    // step s's inputs into LDS: x, and for the RMSNorm
+                    // prologue x2 and gamma (1 KB per instruction; lanes past
+                    // the end re-read the last 16 bytes)
+                    const ChainStepDev& st = steps[s];
+                    const int nb = st.K * 2;
+                    const int kpb = (nb + 1023) & ~1023;
+                    const uint32_t sb = lds_addr(stage);
+                    for (int c = 0; c < kpb; c += 1024) {
+                        const int off = min(c + lane * 16, nb - 16);
+                        dma16_coh(reinterpret_cast<const char*>(st.X) + off, sb + c);
+                    }
+                    if (st.pro == 2) {
+                        const uint16_t* x2 = st.x2 ? st.x2 : st.X;
+                        for (int c = 0; c < kpb; c += 1024) {
+                            const int off = min(c + lane * 16, nb - 16);
+                            dma16_coh(reinterpret_cast<const char*>(x2) + off, sb + kpb + c);
+                            dma16(reinterpret_cast<const char*>(st.gamma) + off, sb + 2 * kpb + c);
+                        }
+                    }
+                    wait_vm<0>();
+                }
+                tr(s, 3);
             }
-            __syncthreads();
-            if (__builtin_amdgcn_readfirstlane(ctl_s[1]) != 0) break;
-            const uint16_t* const X = st.X;
-            v4i xr[XV];
+            if (lane == 0) ctl_s[0] = status;
+        }
+        __syncthreads();   // B: inputs of step s in LDS (or a wait gave up)
+        if (s == nsteps || ufirst(ctl_s[0]) != 0) break;
+
+        // ---- prologue of step s: its int8 codes and group scales in LDS
+        const ChainStepDev& st = steps[s];
+        const int K = st.K, lg_g = st.lg_g;
+        const int kpb = (K * 2 + 1023) & ~1023;
+        uint16_t* const xst = reinterpret_cast<uint16_t*>(stage);
+        // chunk round i of this wave holds any of x[0, K) (wave-uniform)
+        auto live_chunks = [&](int i) { return (i * NTS + wave * 64) * 8 < K; };
+        v4i xr[XV];
+        if (!ctrl) {
 #pragma unroll
             for (int i = 0; i < XV; ++i) {
-                const int k = (tid + i * NT) * 8;
-                xr[i] = ld16_act(X + (k < K ? k : K - 8));
+                const int k = (tid + i * NTS) * 8;
+                xr[i] = k < K ? *reinterpret_cast<const v4i*>(xst + k) : zero;
             }
-            if (st.pro == 2) {
-                v4i x2r[XV2], gmr[XV2];
-                const uint16_t* const x2 = st.x2 ? st.x2 : X;
+        }
+        if (st.pro == 2) {
+            const uint16_t* const x2s = reinterpret_cast<const uint16_t*>(stage + kpb);
+            const uint16_t* const gms = reinterpret_cast<const uint16_t*>(stage + 2 * kpb);
+            if (!ctrl && st.x2) {
+                // h = fp16(x + x2), written back in place
 #pragma unroll
-                for (int i = 0; i < XV2; ++i) {
-                    const int k = (tid + i * NT) * 8;
-                    const int kc = k < K ? k : K - 8;
-                    x2r[i] = ld16_act(x2 + kc);
-                    gmr[i] = ld16c(reinterpret_cast<const int8_t*>(st.gamma + kc));
-                }
-                // h = fp16(x + x2) into LDS (and to h_out from the owner of block 0)
-#pragma unroll
-                for (int i = 0; i < XV2; ++i) {
-                    const int k = (tid + i * NT) * 8;
-                    uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
-                    if (st.x2) {
-                        const uint16_t* r = reinterpret_cast<const uint16_t*>(&x2r[i]);
+                for (int i = 0; i < XV; ++i) {
+                    const int k = (tid + i * NTS) * 8;
+                    if (live_chunks(i) && k < K) {
+                        uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
+                        const v4i rv = *reinterpret_cast<const v4i*>(x2s + k);
+                        const uint16_t* r = reinterpret_cast<const uint16_t*>(&rv);
 #pragma unroll
                         for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(h[e]) + h2f(r[e]));
-                    }
-                    if (k < K) {
-                        *reinterpret_cast<v4i*>(h_s + k) = xr[i];
-                        if (st.h_out && b == 0) st16_coh(st.h_out + k, xr[i]);
+                        *reinterpret_cast<v4i*>(xst + k) = xr[i];
                     }
                 }
-                __syncthreads();
-                // Sum of squares in the reference's order (rms_norm.cu:22-41):
-                // T = min(next_pow2(K), 1024) threads, thread t sums h[t],
-                // h[t + T], ... with FMAs, each 32-thread warp reduces by the
-                // shuffle-down tree, then the warp sums by the same tree.
-                int T = 1;
-                while (T < K) T <<= 1;
-                if (T > 1024) T = 1024;
-                const int lanes = T < 32 ? 32 : T;
-                for (int t0 = 0; t0 < lanes; t0 += NT) {
+            }
+            __syncthreads();
+            if (ctrl && b == 0 && st.h_out) {
+                for (int k = lane * 8; k < K; k += 64 * 8)
+                    st16_coh(st.h_out + k, *reinterpret_cast<const v4i*>(xst + k));
+            }
+            // Sum of squares in the reference's order (rms_norm.cu:22-41):
+            // T = min(next_pow2(K), 1024) threads, thread t sums h[t],
+            // h[t + T], ... with FMAs, each 32-thread warp reduces by the
+            // shuffle-down tree, then the warp sums by the same tree.
+            int T = 1;
+            while (T < K) T <<= 1;
+            if (T > 1024) T = 1024;
+            const int lanes = T < 32 ? 32 : T;
+            if (!ctrl) {
+                for (int t0 = 0; t0 < lanes; t0 += NTS) {
                     const int tt = t0 + tid;
                     float loc = 0.0f;
                     if (tt < T)
                         for (int k = tt; k < K; k += T) {
-                            const float v = h2f(h_s[k]);
+                            const float v = h2f(xst[k]);
                             loc = __builtin_fmaf(v, v, loc);
                         }
                     loc = warp32_sum_down(loc);
                     if (tt < lanes && (tt & 31) == 0) red_s[tt >> 5] = loc;
                 }
-                __syncthreads();
-                if (tid < 32) {
-                    const int nw = (T + 31) >> 5;
-                    float v = tid < nw ? red_s[tid] : 0.0f;
-                    v = warp32_sum_down(v);
-                    if (tid == 0) red_s[32] = rms_inv(v, K, st.eps);
-                }
-                __syncthreads();
-                const float rr = red_s[32];
+            }
+            __syncthreads();
+            if (tid < 32) {
+                const int nw = (T + 31) >> 5;
+                float v = tid < nw ? red_s[tid] : 0.0f;
+                v = warp32_sum_down(v);
+                if (tid == 0) red_s[32] = rms_inv(v, K, st.eps);
+            }
+            __syncthreads();
+            const float rr = red_s[32];
+            if (!ctrl) {
 #pragma unroll
-                for (int i = 0; i < XV2; ++i) {
-                    uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
-                    const uint16_t* gm = reinterpret_cast<const uint16_t*>(&gmr[i]);
+                for (int i = 0; i < XV; ++i) {
+                    const int k = (tid + i * NTS) * 8;
+                    if (live_chunks(i) && k < K) {
+                        uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
+                        const v4i gv = *reinterpret_cast<const v4i*>(gms + k);
+                        const uint16_t* gm = reinterpret_cast<const uint16_t*>(&gv);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) h[e] = f2h((h2f(h[e]) * rr) * h2f(gm[e]));
+                        for (int e = 0; e < 8; ++e) h[e] = f2h((h2f(h[e]) * rr) * h2f(gm[e]));
+                    }
                 }
             }
+        }
+        if (!ctrl) {
             // Per-group dynamic quantization: chunk c = x[8c, 8c + 8) sits in
-            // thread c % NT, so a group's g / 8 chunks are consecutive lanes of
-            // one wave; their |v| max comes from DPP / shuffles.
+            // thread c % NTS, so a group's g / 8 chunks are consecutive lanes
+            // of one wave; their |v| max comes from DPP / shuffles.
 #pragma unroll
             for (int i = 0; i < XV; ++i) {
-                const int c = tid + i * NT;
+                if (!live_chunks(i)) continue;   // no chunk of this wave reaches K
+                const int c = tid + i * NTS;
                 const int k = c * 8;
                 const bool ok = k < K;
                 const uint16_t* h = reinterpret_cast<const uint16_t*>(&xr[i]);
@@ -375,146 +547,176 @@ __global__ __launch_bounds__(NWV * 64) void chain_kernel(const ChainStepDev* __r
                     if ((c & ((1 << (lg_g - 3)) - 1)) == 0) xs_s[k >> lg_g] = scl;
                 }
             }
-            __syncthreads();
-            prepared = s;
         }
+        __syncthreads();   // C: codes ready; the input staging is free for terms
+        tr(s, 4);
 
-        // ---- the block's passes, KD per round; each consumed slot is
-        // refilled with pass + KD of this block or, past its padded end,
-        // with the next block's first passes (selected, not branched)
-        const Blk nxt = next_of(cur);
-        const RowPtr rc = row_ptr(cur), rn = row_ptr(nxt);
-        float acc[R] = {0.0f, 0.0f};
-        for (int base = 0; base < cur.P; base += KD) {
-#pragma unroll
-            for (int q = 0; q < KD; ++q) {
-                const int kbase = (base + q) * PB;
-                const int k = kbase + lane_k;
-                v4i bq = *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
-                if (k >= K) bq = zero;
-                int p = __builtin_amdgcn_sdot4(a[q].x, bq.x, 0, false);
-                p = __builtin_amdgcn_sdot4(a[q].y, bq.y, p, false);
-                p = __builtin_amdgcn_sdot4(a[q].z, bq.z, p, false);
-                p = __builtin_amdgcn_sdot4(a[q].w, bq.w, p, false);
+        // ---- the wave's items of step s, UB at a time (independent LDS
+        // reads and dot products in flight together), then one by one
+        if (!ctrl) {
+            start(cs, s);
+            int pa, pb;
+            wg_pairs(cs.c.M, pa, pb);
+            const int nr = 2 * (pb - pa);     // term table row stride
+            auto item = [&](int sl, int pl, int pass, float& term, int& tix) {
+                const uint32_t base = (uint32_t)(wave * DEPTH + sl) * kSlot;
+                const v4i wv = *reinterpret_cast<const v4i*>(smem + base + lane * 16);
+                const uint32_t sw =
+                    *reinterpret_cast<const uint32_t*>(smem + base + 1024 + lane * 4);
+                const int k = pass * PB + lk;
+                const bool live = k < cs.c.K;
+                const v4i xq = *reinterpret_cast<const v4i*>(xq_s + (live ? k : 0));
+                int p = __builtin_amdgcn_sdot4(wv.x, xq.x, 0, false);
+                p = __builtin_amdgcn_sdot4(wv.y, xq.y, p, false);
+                p = __builtin_amdgcn_sdot4(wv.z, xq.z, p, false);
+                p = __builtin_amdgcn_sdot4(wv.w, xq.w, p, false);
                 p = lane_group_sum<LG>(p);
-                const float term = (float)p * h2f(sc[q]);
-                float xsv[GPP];
-                const float* xp = xs_s + (kbase >> lg_g);
-#pragma unroll
-                for (int j = 0; j < GPP; ++j) xsv[j] = xp[j];
-#pragma unroll
-                for (int j = 0; j < GPP; ++j) {
-                    if (kbase + j * LG * 16 < K) {
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const float tj = __builtin_bit_cast(
-                                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
-                                                                 r * RL + j * LG));
-                            acc[r] = __builtin_fmaf(tj, xsv[j], acc[r]);
-                        }
-                    }
+                int row = 2 * (cs.pa + pl) + rsub;
+                row = row < cs.c.M ? row : cs.c.M - 1;
+                const int kk = live ? k : 0;
+                const int idx = row * cs.c.G + (kk >> cs.c.lg);
+                int lo = idx & ~1;
+                lo = lo < cs.c.mg2 ? lo : cs.c.mg2;
+                const uint16_t ws = (uint16_t)(idx != lo ? sw >> 16 : sw & 0xffffu);
+                term = (float)p * h2f(ws);
+                // only the group leader of a live group stores its term
+                tix = (live && (lane & (LG - 1)) == 0) ? (k >> cs.c.lg) * nr + 2 * pl + rsub : -1;
+            };
+            auto step_pos = [&](int& pl, int& pass) {
+                if (++pass == cs.c.passes) {
+                    pass = 0;
+                    ++pl;
                 }
-                const int np = base + q + KD;
-                const bool here = np < cur.P;
-                RowPtr rp;
-                rp.w = here ? rc.w : rn.w;
-                rp.ws = here ? rc.ws : rn.ws;
-                rp.K = here ? rc.K : rn.K;
-                rp.lg_g = here ? rc.lg_g : rn.lg_g;
-                load(q, rp, here ? np : np - cur.P);
-            }
-        }
-
-        // ---- outputs: staged in LDS, stored by wave 0 (agent-coherent)
-        {
-            uint16_t* const y_s = y_s0 + (fin & 1) * ROWS;
-            ++fin;
-            if (lane == 0) {
-                if (st.epi == 1) {
-                    y_s[wave] = f2h(h2f(f2h(silu_f(h2f(f2h(acc[0]))))) * h2f(f2h(acc[1])));
-                } else {
-                    y_s[2 * wave] = f2h(acc[0]);
-                    y_s[2 * wave + 1] = f2h(acc[1]);
+            };
+            constexpr int UB = 4;
+            while (cs.rem >= UB) {
+                wait_vm<NOPS * (DEPTH - UB)>();   // items it .. it + 3 landed
+                float t[UB];
+                int ti[UB];
+                int pl = cs.pl, pass = cs.pass, sl = slot;
+#pragma unroll
+                for (int u = 0; u < UB; ++u) {
+                    item(sl, pl, pass, t[u], ti[u]);
+                    step_pos(pl, pass);
+                    sl = sl + 1 == DEPTH ? 0 : sl + 1;
                 }
+#pragma unroll
+                for (int u = 0; u < UB; ++u)
+                    if (ti[u] >= 0) terms[ti[u]] = t[u];
+                wait_lgkm0();   // the slots' reads are done before they are refilled
+#pragma unroll 1
+                for (int u = 0; u < UB; ++u) {
+                    issue(slot);
+                    slot = slot + 1 == DEPTH ? 0 : slot + 1;
+                }
+                cs.pl = ufirst(pl);
+                cs.pass = ufirst(pass);
+                cs.rem -= UB;
             }
-            __syncthreads();
-            const int per = st.epi == 1 ? ROWS / 2 : ROWS;
-            const int total_out = st.epi == 1 ? M / 2 : M;
-            const int ob = cur.blk * per;
-            const int cnt = min(per, total_out - ob);
-            if (tid < (cnt + 1) / 2) {
-                uint16_t* dst = st.Y + ob + 2 * tid;
-                if (2 * tid + 1 < cnt)
-                    __hip_atomic_store(g32(dst),
-                                       (uint32_t)y_s[2 * tid] | ((uint32_t)y_s[2 * tid + 1] << 16),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else
-                    st2_coh(dst, y_s[2 * tid]);
+            while (cs.rem > 0) {
+                wait_vm<NOPS * (DEPTH - 1)>();   // the item has landed
+                float t0;
+                int ti0;
+                item(slot, cs.pl, cs.pass, t0, ti0);
+                if (ti0 >= 0) terms[ti0] = t0;
+                wait_lgkm0();
+                issue(slot);
+                slot = slot + 1 == DEPTH ? 0 : slot + 1;
+                step_pos(cs.pl, cs.pass);
+                --cs.rem;
             }
-            ++done_here;
         }
-        if (nxt.s >= nsteps) {
-            signal(cur.s);
-            break;
-        }
-        cur = nxt;
     }
-    stores_done();
+    wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
 }
 
-__global__ void chain_zero_kernel(int* p, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+__global__ void chain_zero_kernel(int* a, int na, int* c, int nc) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < na; i += gridDim.x * blockDim.x)
+        a[i] = 0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nc; i += gridDim.x * blockDim.x)
+        c[i] = 0;
 }
 
-template <int LG>
-hipError_t launch_lg(const ChainPlan& p, hipStream_t stream) {
-    hipLaunchKernelGGL(chain_zero_kernel, dim3(1), dim3(256), 0, stream, p.sync, p.nsteps + 1);
-    const ChainStepDev* steps = p.steps;
-    int nsteps = p.nsteps, spin = p.spin_limit, kp = p.kp_max, gp = p.g_pad, kh = p.kh;
-    int* sync = p.sync;
-    int* flags = p.flags;
-    int epoch = p.epoch;
-    void* args[] = {&steps, &nsteps, &sync, &flags, &epoch, &spin, &kp, &gp, &kh};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(chain_kernel<LG, kChainWaves>),
-                                      dim3((unsigned)p.grid), dim3(kChainWaves * 64), args, p.lds,
-                                      stream);
+template <int LG, int DEPTH>
+void* kernel_ptr() {
+    return reinterpret_cast<void*>(chain_kernel<LG, DEPTH, kPrefetch, kTrace>);
 }
-
-template <int LG>
-int grid_lg(size_t lds) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, chain_kernel<LG, kChainWaves>,
-                                                     kChainWaves * 64, lds) != hipSuccess)
-        return 0;
-    return cus * per_cu;
+template <int DEPTH>
+void* kernel_for(int lg) {
+    if (lg == 6) return kernel_ptr<4, DEPTH>();
+    if (lg == 7) return kernel_ptr<8, DEPTH>();
+    if (lg == 8) return kernel_ptr<16, DEPTH>();
+    return nullptr;
+}
+void* kernel_for(int lg, int depth) {
+    if (depth == 12) return kernel_for<12>(lg);
+    if (depth == 8) return kernel_for<8>(lg);
+    return nullptr;
 }
 
 }  // namespace
 
-size_t chain_lds_bytes(int kp_max, int g_pad, int kh) {
-    return (size_t)kp_max + (size_t)g_pad * 4 + (size_t)kh * 2 + 36 * 4 +
-           (size_t)2 * kChainWaves * R * 2;
+ch::ChainLds chain_lds(int depth, int kp_max, int kh, int g_pad, int term_floats) {
+    ch::ChainLds l{};
+    int off = NS * depth * kSlot;
+    l.xq = off;
+    off += (kp_max + 15) & ~15;
+    l.xs = off;
+    off += ((g_pad + 3) & ~3) * 4;
+    l.stage = off;
+    const int kpb = (kp_max * 2 + 1023) & ~1023;
+    const int kpbh = (kh * 2 + 1023) & ~1023;
+    int st = kpb;
+    if (3 * kpbh > st) st = 3 * kpbh;
+    if (term_floats * 4 > st) st = term_floats * 4;
+    off += (st + 15) & ~15;
+    l.red = off;
+    off += 64 * 4 + 256;   // reduction words, status, prefetch landing
+    l.total = off;
+    return l;
 }
 
-int chain_rows_per_task() { return kChainWaves * R; }
+int chain_depth_for(int lds_total_at_depth8) {
+    // the deeper ring when its 8 * 4 extra slots per wave still fit in 160 KB
+    return lds_total_at_depth8 + NS * 4 * kSlot <= 160 * 1024 ? 12 : 8;
+}
+
+int chain_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return cus;
+}
+
+int chain_grid(int lg, int depth, size_t lds) {
+    void* k = kernel_for(lg, depth);
+    if (!k) return 0;
+    // raise the dynamic LDS limit where the runtime keeps one (the result is
+    // checked through the occupancy query below)
+    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTH, lds) != hipSuccess) return 0;
+    return chain_cus() * per_cu;
+}
+
 int chain_max_k() { return kChainMaxK; }
 int chain_max_k_pro() { return kChainMaxKPro; }
 
-int chain_grid(int lg, size_t lds) {
-    if (lg == 6) return grid_lg<4>(lds);
-    if (lg == 7) return grid_lg<8>(lds);
-    if (lg == 8) return grid_lg<16>(lds);
-    return 0;
-}
-
 hipError_t launch_chain(const ChainPlan& p, hipStream_t stream) {
-    if (p.lg == 6) return launch_lg<4>(p, stream);
-    if (p.lg == 7) return launch_lg<8>(p, stream);
-    if (p.lg == 8) return launch_lg<16>(p, stream);
-    return hipErrorInvalidValue;
+    void* k = kernel_for(p.lg, p.depth);
+    if (!k) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(chain_zero_kernel, dim3(64), dim3(256), 0, stream, p.flags,
+                       p.nsteps * 8 * 32, p.sync, p.nsteps + 1);
+    const ChainStepDev* steps = p.steps;
+    int nsteps = p.nsteps, spin = p.spin_limit;
+    int* sync = p.sync;
+    int* flags = p.flags;
+    ch::ChainLds lay = p.lay;
+    unsigned long long* trace = p.trace;
+    void* args[] = {&steps, &nsteps, &sync, &flags, &spin, &lay, &trace};
+    return hipLaunchKernel(k, dim3((unsigned)p.grid), dim3(NTH), args, (size_t)p.lay.total,
+                           stream);
 }
 
 }  // namespace fa

@@ -105,6 +105,171 @@ __device__ __forceinline__ float block_max(float m, int lgl) {
     return m;
 }
 
+// ---------------------------------------------------- in-kernel quant ----
+//
+// The fp16 token a one-token kernel quantizes itself (QX), in two halves so
+// the caller can put its weight loads in between: qx_load issues the
+// activation loads (XV 16-byte chunks of 8 fp16 values per thread, chunk c =
+// tid + i * NT), qx_stage applies the fused prologue and writes the int8
+// codes to xq_s [K] and the group scales to xs_s [G] (int8_gemm.cu:147-211
+// semantics: per-group amax/127 or a static scale, optional smooth_inv).
+template <int XV, int PRO>
+struct QxIn {
+    v4i xr[XV];
+    v4i x2r[PRO != 0 ? XV : 1];
+    v4i gmr[PRO == 2 ? XV : 1];
+};
+
+template <int XV, int NT, int PRO>
+__device__ __forceinline__ void qx_load(QxIn<XV, PRO>& in, const uint16_t* __restrict__ X, int K,
+                                        const ProArgs& pro, int tid) {
+    // unconditional loads from clamped addresses (a load under a branch
+    // makes the compiler wait for it on the spot)
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int k = (tid + i * NT) * 8;
+        in.xr[i] = *reinterpret_cast<const v4i*>(X + (k < K ? k : K - 8));
+    }
+    // prologue operands: up (PRO 1) or the residual addend (PRO 2; X again
+    // when there is none) and gamma
+    if constexpr (PRO != 0) {
+        const uint16_t* x2 = pro.x2 ? pro.x2 : X;
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int k = (tid + i * NT) * 8;
+            const int kc = k < K ? k : K - 8;
+            in.x2r[i] = *reinterpret_cast<const v4i*>(x2 + kc);
+            if constexpr (PRO == 2) in.gmr[i] = *reinterpret_cast<const v4i*>(pro.gamma + kc);
+        }
+    }
+}
+
+// write_h: this workgroup writes h to pro.h_out (PRO 2).  Contains workgroup
+// barriers (PRO 2): every thread of the workgroup must call it.  The caller
+// synchronises before reading xq_s / xs_s.
+template <int XV, int NT, int PRO>
+__device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __restrict__ X,
+                                         const uint16_t* __restrict__ act_scale,
+                                         const uint16_t* __restrict__ smooth_inv, int K, int lg_g,
+                                         int G, const ProArgs& pro, int tid, bool write_h,
+                                         int8_t* xq_s, float* xs_s, uint16_t* h_s, float* red_s) {
+    // Chunk c holds x[8c, 8c + 8); chunk c of thread tid is tid + i * NT,
+    // so a K-group (g / 8 chunks) lies in g / 8 consecutive lanes of one
+    // wave.  Its |v| maximum (exact in any order) comes from xor shuffles,
+    // then scale and int8 codes are formed in registers: no atomics and a
+    // single barrier (the caller's) before the codes are read.
+    const int glanes = 1 << (lg_g - 3);
+    auto chunk = [&](int c, const v4i& raw) {
+        const int k = c * 8;
+        const bool ok = k < K;
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[e] = h2f(h[e]);
+            if (smooth_inv) v[e] *= h2f(smooth_inv[ok ? k + e : e]);
+        }
+        const int gi = ok ? k >> lg_g : G - 1;
+        float sc_;
+        if (act_scale) {
+            sc_ = h2f(act_scale[gi]);
+            sc_ = sc_ < 1e-8f ? 1e-8f : sc_;
+        } else {
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+            if (!ok) m = 0.0f;
+            m = block_max(m, lg_g - 3);
+            sc_ = act_scale_from_amax(m);
+        }
+        if (ok) {
+            const float inv = 1.0f / sc_;
+            int q[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
+            uint2 u;
+            u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                  ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+            u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
+                  ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
+            *reinterpret_cast<uint2*>(xq_s + k) = u;
+            if ((c & (glanes - 1)) == 0) xs_s[gi] = sc_;
+        }
+    };
+    if constexpr (PRO == 1) {
+        // silu_forward then mul_forward, each rounded to fp16
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            uint16_t* h = reinterpret_cast<uint16_t*>(&in.xr[i]);
+            const uint16_t* u = reinterpret_cast<const uint16_t*>(&in.x2r[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(f2h(silu_f(h2f(h[e])))) * h2f(u[e]));
+        }
+    } else if constexpr (PRO == 2) {
+        // h = fp16(x + resid) into LDS (and to h_out from one workgroup)
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int k = (tid + i * NT) * 8;
+            uint16_t* h = reinterpret_cast<uint16_t*>(&in.xr[i]);
+            if (pro.x2) {
+                const uint16_t* r = reinterpret_cast<const uint16_t*>(&in.x2r[i]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(h[e]) + h2f(r[e]));
+            }
+            if (k < K) {
+                *reinterpret_cast<v4i*>(h_s + k) = in.xr[i];
+                if (pro.h_out && write_h) *reinterpret_cast<v4i*>(pro.h_out + k) = in.xr[i];
+            }
+        }
+        __syncthreads();
+        // Sum of squares in the reference's order (rms_norm.cu:22-41):
+        // T = min(next_pow2(K), 1024) threads, thread t sums h[t],
+        // h[t + T], ... with FMAs, each 32-thread warp reduces by the
+        // shuffle-down tree, then the warp sums by the same tree.  Thread
+        // tid plays threads tid, tid + NT, ...
+        int T = 1;
+        while (T < K) T <<= 1;
+        if (T > 1024) T = 1024;
+        const int lanes = T < 32 ? 32 : T;
+        for (int t0 = 0; t0 < lanes; t0 += NT) {      // uniform trip count
+            const int t = t0 + tid;
+            float loc = 0.0f;
+            if (t < T)
+                for (int k = t; k < K; k += T) {
+                    const float v = h2f(h_s[k]);
+                    loc = __builtin_fmaf(v, v, loc);
+                }
+            loc = warp32_sum_down(loc);
+            if (t < lanes && (t & 31) == 0) red_s[t >> 5] = loc;
+        }
+        __syncthreads();
+        if (tid < 32) {
+            const int nw = (T + 31) >> 5;
+            float v = tid < nw ? red_s[tid] : 0.0f;
+            v = warp32_sum_down(v);
+            if (tid == 0) red_s[32] = rms_inv(v, K, pro.eps);
+        }
+        __syncthreads();
+        const float rr = red_s[32];
+        // normalised fp16 row (rms_norm.cu:52-56)
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            uint16_t* h = reinterpret_cast<uint16_t*>(&in.xr[i]);
+            const uint16_t* gm = reinterpret_cast<const uint16_t*>(&in.gmr[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f2h((h2f(h[e]) * rr) * h2f(gm[e]));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < XV; ++i) chunk(tid + i * NT, in.xr[i]);
+    if constexpr (PRO == 0) {
+        for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
+            const int c = c0 + tid;
+            chunk(c, *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8)));
+        }
+    }
+}
+
 // One wave streams R rows (R = 1, 2 or 4; 64/R lanes per row, 16 bytes per
 // lane per pass).  After 4 v_dot4 per lane, lanes of one K-group (LG = g/16
 // of them) sum their partials with DPP, so every lane of a group holds the
@@ -174,6 +339,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     // the compiler wait for it on the spot).
     v4i xr[XV];
     float xsr = 0.0f;
+    QxIn<XV, PRO> qin;
     if constexpr (!QX) {
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
@@ -182,24 +348,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         }
         xsr = x_scale[tid < G ? tid : G - 1];
     } else {
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int k = (tid + i * NT) * 8;
-            xr[i] = *reinterpret_cast<const v4i*>(X + (k < K ? k : K - 8));
-        }
-    }
-    // prologue operands: up (PRO 1) or the residual addend (PRO 2; X again
-    // when there is none) and gamma
-    v4i x2r[PRO != 0 ? XV : 1], gmr[PRO == 2 ? XV : 1];
-    if constexpr (PRO != 0) {
-        const uint16_t* x2 = pro.x2 ? pro.x2 : X;
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int k = (tid + i * NT) * 8;
-            const int kc = k < K ? k : K - 8;
-            x2r[i] = *reinterpret_cast<const v4i*>(x2 + kc);
-            if constexpr (PRO == 2) gmr[i] = *reinterpret_cast<const v4i*>(pro.gamma + kc);
-        }
+        qx_load<XV, NT, PRO>(qin, X, K, pro, tid);
     }
 
     // ---- weight ring
@@ -246,121 +395,8 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
             *reinterpret_cast<v4i*>(xq_s + k) = ld16(x_q + k);
         for (int i = tid + NT; i < G; i += NT) xs_s[i] = x_scale[i];
     } else {
-        // Chunk c holds x[8c, 8c + 8); chunk c of thread tid is tid + i * NT,
-        // so a K-group (g / 8 chunks) lies in g / 8 consecutive lanes of one
-        // wave.  Its |v| maximum (exact in any order) comes from xor
-        // shuffles, then scale and int8 codes are formed in registers: no
-        // atomics and a single barrier before the codes are read.
-        const int glanes = 1 << (lg_g - 3);
-        auto chunk = [&](int c, const v4i& raw) {
-            const int k = c * 8;
-            const bool ok = k < K;
-            const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                v[e] = h2f(h[e]);
-                if (smooth_inv) v[e] *= h2f(smooth_inv[ok ? k + e : e]);
-            }
-            const int gi = ok ? k >> lg_g : G - 1;
-            float sc_;
-            if (act_scale) {
-                sc_ = h2f(act_scale[gi]);
-                sc_ = sc_ < 1e-8f ? 1e-8f : sc_;
-            } else {
-                float m = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-                if (!ok) m = 0.0f;
-                m = block_max(m, lg_g - 3);
-                sc_ = act_scale_from_amax(m);
-            }
-            if (ok) {
-                const float inv = 1.0f / sc_;
-                int q[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) q[e] = quant_rn(v[e], inv);
-                uint2 u;
-                u.x = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                      ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
-                u.y = (uint32_t)(q[4] & 0xff) | ((uint32_t)(q[5] & 0xff) << 8) |
-                      ((uint32_t)(q[6] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24);
-                *reinterpret_cast<uint2*>(xq_s + k) = u;
-                if ((c & (glanes - 1)) == 0) xs_s[gi] = sc_;
-            }
-        };
-        if constexpr (PRO == 1) {
-            // silu_forward then mul_forward, each rounded to fp16
-#pragma unroll
-            for (int i = 0; i < XV; ++i) {
-                uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
-                const uint16_t* u = reinterpret_cast<const uint16_t*>(&x2r[i]);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(f2h(silu_f(h2f(h[e])))) * h2f(u[e]));
-            }
-        } else if constexpr (PRO == 2) {
-            // h = fp16(x + resid) into LDS (and to h_out from workgroup 0)
-#pragma unroll
-            for (int i = 0; i < XV; ++i) {
-                const int k = (tid + i * NT) * 8;
-                uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
-                if (pro.x2) {
-                    const uint16_t* r = reinterpret_cast<const uint16_t*>(&x2r[i]);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) h[e] = f2h(h2f(h[e]) + h2f(r[e]));
-                }
-                if (k < K) {
-                    *reinterpret_cast<v4i*>(h_s + k) = xr[i];
-                    if (pro.h_out && blockIdx.x == 0) *reinterpret_cast<v4i*>(pro.h_out + k) = xr[i];
-                }
-            }
-            __syncthreads();
-            // Sum of squares in the reference's order (rms_norm.cu:22-41):
-            // T = min(next_pow2(K), 1024) threads, thread t sums h[t],
-            // h[t + T], ... with FMAs, each 32-thread warp reduces by the
-            // shuffle-down tree, then the warp sums by the same tree.  Thread
-            // tid plays threads tid, tid + NT, ...
-            int T = 1;
-            while (T < K) T <<= 1;
-            if (T > 1024) T = 1024;
-            const int lanes = T < 32 ? 32 : T;
-            for (int t0 = 0; t0 < lanes; t0 += NT) {      // uniform trip count
-                const int t = t0 + tid;
-                float loc = 0.0f;
-                if (t < T)
-                    for (int k = t; k < K; k += T) {
-                        const float v = h2f(h_s[k]);
-                        loc = __builtin_fmaf(v, v, loc);
-                    }
-                loc = warp32_sum_down(loc);
-                if (t < lanes && (t & 31) == 0) red_s[t >> 5] = loc;
-            }
-            __syncthreads();
-            if (tid < 32) {
-                const int nw = (T + 31) >> 5;
-                float v = tid < nw ? red_s[tid] : 0.0f;
-                v = warp32_sum_down(v);
-                if (tid == 0) red_s[32] = rms_inv(v, K, pro.eps);
-            }
-            __syncthreads();
-            const float rr = red_s[32];
-            // normalised fp16 row (rms_norm.cu:52-56)
-#pragma unroll
-            for (int i = 0; i < XV; ++i) {
-                uint16_t* h = reinterpret_cast<uint16_t*>(&xr[i]);
-                const uint16_t* gm = reinterpret_cast<const uint16_t*>(&gmr[i]);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = f2h((h2f(h[e]) * rr) * h2f(gm[e]));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < XV; ++i) chunk(tid + i * NT, xr[i]);
-        if constexpr (PRO == 0) {
-            for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
-                const int c = c0 + tid;
-                chunk(c, *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8)));
-            }
-        }
+        qx_stage<XV, NT, PRO>(qin, X, act_scale, smooth_inv, K, lg_g, G, pro, tid,
+                              blockIdx.x == 0, xq_s, xs_s, h_s, red_s);
     }
     if constexpr ((kAb & 1) == 0) __syncthreads();
 

@@ -5,7 +5,11 @@ Loading fails loudly: there is no CPU or PyTorch fallback for any entry point.
 import ctypes
 import os
 
-from .build import LIB_PATH
+from .build import LIB_PATH as _BUILT_LIB
+
+# FISH_W8A8_LIB selects another build of the library (e.g. a measurement
+# build); by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("FISH_W8A8_LIB") or _BUILT_LIB
 
 FA_OK = 0
 FA_ERR_INVALID_ARG = 1

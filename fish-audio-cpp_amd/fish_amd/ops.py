@@ -338,9 +338,10 @@ class Chain:
     def __del__(self):
         # at interpreter exit the HIP runtime may already be gone: leave the
         # device memory to the process teardown
-        if sys.is_finalizing():
-            return
+        # (module globals such as `sys` may already be None then)
         try:
+            if sys.is_finalizing():
+                return
             self.close()
         except Exception:
             pass
