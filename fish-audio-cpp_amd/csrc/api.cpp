@@ -57,7 +57,11 @@ struct Workspace {
     size_t st_bytes = 0;
     uint16_t* yt = nullptr;     // fp16 [N, 2F] of the SwiGLU entry's separate-launch path
     size_t yt_bytes = 0;
+    int* sk = nullptr;          // prefill K split: kSplitCounters zeroed ints, then partials
+    size_t sk_bytes = 0;
 };
+
+constexpr size_t kSplitCounters = 16384;   // tiles a split launch may have
 
 thread_local std::unordered_map<int, Workspace> g_ws;
 
@@ -101,6 +105,7 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
     }
     const bool tile = aligned && fa::gemm_tile_ok(M, N, K, g);
     if (tile || (aligned && fa::gemm_pipe_ok(M, N, K, g))) {
+        const bool own_tables = tables == nullptr;
         if (!tables) {
             Workspace* ws = nullptr;
             int rc = current_ws(&ws);
@@ -111,9 +116,33 @@ int linear_quantized(const char* fn, const int8_t* W, const uint16_t* w_scale, i
             if (rc) return rc;
             tables = ws->st;
         }
-        if (tile)
+        if (tile) {
+            // K split for few-tile grids, on the thread's scratch only (the
+            // no-alloc entry runs unsplit)
+            const int variant = fa::gemm_tile_choice(M, N, K, g);
+            int nsplit = own_tables ? fa::gemm_tile_split(M, N, K, g, variant) : 1;
+            float* part = nullptr;
+            int* cnt = nullptr;
+            if (nsplit > 1) {
+                Workspace* ws = nullptr;
+                int rc = current_ws(&ws);
+                if (rc) return rc;
+                const size_t need = kSplitCounters * sizeof(int) +
+                                    fa::gemm_tile_split_bytes(M, N, variant, nsplit);
+                if (ws->sk_bytes < need) {
+                    void* p = ws->sk;
+                    rc = grow(&p, &ws->sk_bytes, need, stream);
+                    ws->sk = (int*)p;
+                    if (rc) return rc;
+                    // counters start at zero; every launch leaves them so
+                    FA_HIP(hipMemsetAsync(ws->sk, 0, kSplitCounters * sizeof(int), stream));
+                }
+                cnt = ws->sk;
+                part = reinterpret_cast<float*>(ws->sk + kSplitCounters);
+            }
             FA_HIP(fa::launch_gemm_tile(W, w_scale, xq, xs, tables, Y, dbg, row0, rows, tok0, toks,
-                                        M, N, K, g, G, stream));
+                                        M, N, K, g, G, stream, variant, -1, nsplit, part, cnt));
+        }
         else
             FA_HIP(fa::launch_gemm_pipe(W, w_scale, xq, xs, tables, Y, dbg, row0, rows, tok0, toks,
                                         M, N, K, g, G, stream));
@@ -167,6 +196,14 @@ int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_s
     const int G = (K + g - 1) / g;
     return linear_quantized(fn, W, w_scale, g, G, X_q, X_scale, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             (hipStream_t)stream);
+}
+
+int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size) {
+    g_err.clear();
+    if (M <= 0 || N <= 16 || K <= 0) return 1;
+    const int g = eff_group(K, group_size);
+    if (!fa::gemm_tile_ok(M, N, K, g)) return 1;
+    return fa::gemm_tile_split(M, N, K, g, fa::gemm_tile_choice(M, N, K, g));
 }
 
 int fa_w8a8_gemm_partials(const int8_t* W, const uint16_t* w_scale, int group_size,
@@ -722,6 +759,19 @@ int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_siz
     rc = grow(&p, &ws->st_bytes, fa::gemm_pipe_tables_bytes(max_M, max_tokens, G), s);
     ws->st = (float*)p;
     if (rc) return rc;
+    if (max_tokens > 16 && ws->sk_bytes == 0) {
+        // prefill K split: a split launch has at most 2 workgroups per CU,
+        // each with a 128 x 128 (or 256 x 128, one per CU) partial tile
+        int dev = 0, cus = 0;
+        FA_HIP(hipGetDevice(&dev));
+        FA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        const size_t need = kSplitCounters * sizeof(int) + (size_t)cus * 2 * 128 * 128 * 4;
+        p = ws->sk;
+        rc = grow(&p, &ws->sk_bytes, need, s);
+        ws->sk = (int*)p;
+        if (rc) return rc;
+        FA_HIP(hipMemsetAsync(ws->sk, 0, kSplitCounters * sizeof(int), s));
+    }
     if (max_tokens > 1) {   // fa_w8a8_gemm_swiglu's [N, 2F] linear output (max_M = 2F)
         p = ws->yt;
         rc = grow(&p, &ws->yt_bytes, (size_t)max_tokens * (size_t)max_M * 2, s);
@@ -741,6 +791,7 @@ int fa_workspace_release(void) {
     if (ws->xs) FA_HIP(hipFree(ws->xs));
     if (ws->st) FA_HIP(hipFree(ws->st));
     if (ws->yt) FA_HIP(hipFree(ws->yt));
+    if (ws->sk) FA_HIP(hipFree(ws->sk));
     *ws = Workspace{};
     return FA_OK;
 }

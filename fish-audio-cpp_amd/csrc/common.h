@@ -188,11 +188,17 @@ bool gemm_tile_ok(int M, int N, int K, int g);
 // scales: -1 = by group size, 0 = group-major tables (extra launch), 1 = gathered
 // in-kernel from the given layouts.
 int gemm_tile_choice(int M, int N, int K, int g);
+// K split over nsplit workgroups per tile (1 = none) for grids with few tiles;
+// the split needs gemm_tile_split_bytes of partial sums plus one zeroed int
+// counter per tile (left zeroed by every launch).
+int gemm_tile_split(int M, int N, int K, int g, int variant = 0);
+size_t gemm_tile_split_bytes(int M, int N, int variant, int nsplit);
 hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                             const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
                             int K, int g, int G, hipStream_t stream, int variant = 0,
-                            int scales = -1);
+                            int scales = -1, int nsplit = 1, float* part = nullptr,
+                            int* tile_cnt = nullptr);
 
 // fp16 x fp16 -> fp16 linear with fp32 accumulation (the FP16 weight path):
 // a streaming GEMV for K % 8 == 0, K <= 4096 and 16-byte aligned W / X

@@ -285,6 +285,18 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
+// Agent-scope (sc1) fp32 store and load: partial sums exchanged between the
+// workgroups of one launch (coherent across the XCDs' L2s).
+typedef __attribute__((address_space(1))) uint32_t gu32_t;
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store((gu32_t*)__builtin_bit_cast(uintptr_t, p), __builtin_bit_cast(uint32_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+    return __builtin_bit_cast(
+        float, __hip_atomic_load((gu32_t*)__builtin_bit_cast(uintptr_t, p), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT));
+}
 
 template <int BM, int BN, int KS, int kNst, int kOcc, bool kDbg, int kAb = 0>
 __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
@@ -570,12 +582,13 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 // x_scale[tok, g].  One gather instruction per wave and group, cheap while a
 // row's G scales are few (g >= 128 here), and no table launch.
 template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, int kAb = 0, bool kSched = true,
-          bool DIRECT = false>
+          bool DIRECT = false, bool SPLIT = false>
 __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ wsT,
     const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G, int tiles_m,
-    int tiles_n, const uint16_t* __restrict__ w_scale, const float* __restrict__ x_scale) {
+    int tiles_n, const uint16_t* __restrict__ w_scale, const float* __restrict__ x_scale,
+    int nsplit, float* __restrict__ part, int* __restrict__ tile_cnt) {
     constexpr int NW = BM * BN / 4096;
     constexpr int WMN = BM / 64;             // waves along the weight rows
     constexpr int AJ = BN * 8 / 64 / NW;     // token-tile loads per wave and stage
@@ -585,6 +598,7 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     constexpr int kPerStage = AJ + BJ + 2;
     constexpr int kYounger = (NST - 2) * kPerStage;
     constexpr int NSS = 8;                   // scale ring: group gi in slot gi & 7
+    constexpr int SPG = 1 << LGS;            // 64-byte substeps per group
     constexpr float kMagicF = 12582912.0f;   // 1.5 * 2^23
     constexpr int kMagicI = 0x4B400000;
 
@@ -659,7 +673,17 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     };
 
     const int nsub = K >> 6;                 // 64-byte substeps
-    const int nst = nsub >> 1;               // 128-byte stages
+    // Split nsplit > 1: this workgroup takes the 128-byte stages [st0,
+    // st0 + nst) of K, whole groups only (units of max(1, g / 128) stages),
+    // and leaves a partial sum for the tile's last finisher to add up.
+    // (SPLIT instances only: the others keep the whole of K, st0 = 0)
+    const int spl = SPLIT ? (int)blockIdx.y : 0;
+    const int unit = SPG >= 2 ? SPG / 2 : 1;
+    const int nunits = (nsub >> 1) / unit;
+    const int st0 = SPLIT ? __builtin_amdgcn_readfirstlane(nunits * spl / nsplit * unit) : 0;
+    const int nst = SPLIT ? __builtin_amdgcn_readfirstlane(nunits * (spl + 1) / nsplit * unit) - st0
+                          : (nsub >> 1);
+    const int gfirst = (2 * st0) >> LGS;     // first group of this split
 
     // Stage st's tiles into ring slot u, plus the scales of the groups that
     // start in stage st (two fetches; a stage with fewer starting groups
@@ -667,7 +691,7 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     // re-fetch the last stage so every wave's load count stays uniform.
     auto issue = [&](int st, int u) {
         if constexpr ((kAb & 8) != 0) return;
-        const int sc_st = min(max(st, 0), nst - 1);
+        const int sc_st = st0 + min(max(st, 0), nst - 1);   // absolute stage
         const size_t koff = (size_t)sc_st * 128;
 #pragma unroll
         for (int j = 0; j < AJ; ++j)
@@ -770,7 +794,9 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
                 if constexpr (kDbg) {
                     const int row = m0 + brow0 + j * 32;
                     const int tok = n0 + wn * 64 + i * 32 + 8 * r + 4 * fh + c;
-                    if (row < M && tok < N && dbg.in(row, tok))
+                    // (a split's first step "finishes" the bare constant of
+                    // the group before its range: not a partial of this split)
+                    if (gi >= gfirst && row < M && tok < N && dbg.in(row, tok))
                         dbg.at(row, tok, gi, G) = P[i][j][e] - kMagicI;
                 }
             }
@@ -789,7 +815,6 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     // One 128-byte stage s held in ring slot U % NST.  U is the stage's index
     // within an unrolled run that starts at an even stage, so the ring slot and
     // every group boundary (SPG substeps per group) are compile-time.
-    constexpr int SPG = 1 << LGS;            // 64-byte substeps per group
     auto stage = [&](auto uc, int s) {
         constexpr int u = decltype(uc)::value;
         if (s < 0) return;   // padding stage before the first run: nothing to do
@@ -799,7 +824,7 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
         issue(s + NST - 1, (u + NST - 1) % NST);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const int tsub = 2 * s + q;
+            const int tsub = 2 * (st0 + s) + q;           // absolute substep
             const bool fresh = ((2 * u + q) % SPG) == 0;   // == (tsub % SPG == 0)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
@@ -901,10 +926,69 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     }
     wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
     // the last group's scales were loaded at its first stage
+    const int glast = (2 * (st0 + nst) - 1) >> LGS;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) epi(G - 1, sv, i, j);
+        for (int j = 0; j < 2; ++j) epi(glast, sv, i, j);
+
+    if constexpr (SPLIT) {
+        // Partial sums of this split to the tile's slot (agent-coherent
+        // stores, value v of thread tid at v * blockDim + tid); the last
+        // split to finish adds all of them in split order (deterministic),
+        // resets the tile's counter and stores the fp16 tile.
+        // (thread index and base made opaque here, so that no address of
+        // this tail is computed ahead of the main loop and held through it)
+        int tid2 = tid;
+        asm volatile("" : "+v"(tid2));
+        const int NTH = (int)blockDim.x;
+        float* pt = part + ((size_t)t * nsplit) * (BM * BN);
+        asm volatile("" : "+s"(pt));
+        float* const mine = pt + (size_t)spl * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    st_coh(mine + (size_t)((i * 2 + j) * 16 + e) * NTH + tid2, acc[i][j][e]);
+        wait_vm<0>();
+        __syncthreads();
+        __shared__ int last_s;
+        if (tid2 == 0) {
+            const int old = __hip_atomic_fetch_add(tile_cnt + t, 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            last_s = old == nsplit - 1;
+        }
+        __syncthreads();
+        if (!last_s) return;
+        // split by split, all 64 values of a split in flight together
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int q = 0; q < nsplit; ++q) {
+            const float* const pq = pt + (size_t)q * (BM * BN) + tid2;
+            float v[2][2][16];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        v[i][j][e] = ld_coh(pq + (size_t)((i * 2 + j) * 16 + e) * NTH);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[i][j][e] += v[i][j][e];
+        }
+        if (tid2 == 0)
+            __hip_atomic_store(tile_cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // fp16 out: lane (row) writes 16 tokens per block; the 32 lanes of a
     // half-wave cover 64 contiguous bytes of one token's output row
@@ -1047,10 +1131,46 @@ int gemm_tile_choice(int M, int N, int K, int g) {
     return (t256 >= 1024 || (K >= 8192 && t256 >= 128)) ? 1 : 2;
 }
 
+int gemm_tile_split(int M, int N, int K, int g, int variant) {
+    // Grids with far fewer tiles than the device holds at once (the o and
+    // down projections at 512 tokens: 80 tiles of 128 x 128 for 256 CUs)
+    // split K over 3 to 8 workgroups per tile, in whole groups.  The fp32 sum
+    // is then formed per split and the splits' sums added in split order, so
+    // the fp16 output is within the reassociation bound of the reference's
+    // single group-ordered chain (int32 partials stay exact).
+    if (variant == 0) variant = gemm_tile_choice(M, N, K, g);
+    if (variant != 2 || g < 128) return 1;   // (the g64 split build spills)
+    const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 1;
+        cus = n;
+    }
+    const int slots = cus * 2;   // two 128 x 128 workgroups per CU
+    if (tiles * 2 > slots) return 1;
+    const int units = (K / 128) / (g >= 256 ? g / 128 : 1);
+    int sp = slots / tiles;
+    if (sp > 8) sp = 8;
+    if (sp > units) sp = units;
+    // (measured on MI355X at 512 tokens, g256: o 28.5 -> 24.9 us and down
+    // 61.1 -> 36.3 us at 6 splits; 2 splits made qkv slower, 21.4 -> 27.9 us)
+    return sp < 3 ? 1 : sp;
+}
+
+size_t gemm_tile_split_bytes(int M, int N, int variant, int nsplit) {
+    const int bm = variant == 1 ? 256 : 128;
+    const size_t tiles = (size_t)ceil_div(M, bm) * ceil_div(N, 128);
+    return tiles * nsplit * bm * 128 * sizeof(float);
+}
+
 hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                             const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,
                             int dbg_row0, int dbg_rows, int dbg_tok0, int dbg_toks, int M, int N,
-                            int K, int g, int G, hipStream_t stream, int variant, int scales) {
+                            int K, int g, int G, hipStream_t stream, int variant, int scales,
+                            int nsplit, float* part, int* tile_cnt) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
     int lg_spg = 0;
     while ((64 << lg_spg) < g) ++lg_spg;
@@ -1064,7 +1184,9 @@ hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8
     // group in its stage wait) by 6-20 %, and at g64 a row has 4x the groups.
     const bool can_direct = (int64_t)M * G >= 2 && ((uintptr_t)w_scale & 3) == 0 &&
                             ((uintptr_t)x_scale & 3) == 0;
-    const bool direct = can_direct && (scales < 0 ? (variant == 2 && g >= 128) : scales == 1);
+    // (split launches take the tables: the gathering build spills once split)
+    const bool direct =
+        can_direct && (scales < 0 ? (variant == 2 && g >= 128 && nsplit == 1) : scales == 1);
     if (!direct) {
         int tr = 64;
         while (tr > 1 && (size_t)tr * G * sizeof(float) > 32768) tr >>= 1;
@@ -1076,31 +1198,41 @@ hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8
     const int bm = variant == 1 ? 256 : 128;
     const int tm = ceil_div(M, bm);
     const int tn = ceil_div(N, 128);
-    const dim3 grid((unsigned)(tm * tn));
-#define FA_TILE_D(BMV, NSTV, OCCV, LGS, DIR)                                                     \
+    if (nsplit < 1 || (nsplit > 1 && (!part || !tile_cnt))) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(tm * tn), (unsigned)nsplit);
+#define FA_TILE_S(BMV, NSTV, OCCV, LGS, DIR, SPL)                                                \
     if (dbg_partials)                                                                            \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true, 0, true, DIR>),    \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true, 0, true, DIR, SPL>), \
                            grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
-                           tm, tn, w_scale, x_scale);                                            \
+                           tm, tn, w_scale, x_scale, nsplit, part, tile_cnt);                    \
     else                                                                                         \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false, 0, true, DIR>),   \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false, 0, true, DIR, SPL>), \
                            grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
-                           tm, tn, w_scale, x_scale);
-#define FA_TILE(BMV, NSTV, OCCV, LGS)                                                            \
-    if (direct) { FA_TILE_D(BMV, NSTV, OCCV, LGS, true) }                                        \
-    else { FA_TILE_D(BMV, NSTV, OCCV, LGS, false) }
-#define FA_TILE_G(BMV, NSTV, OCCV)                                                               \
-    if (lg_spg == 0) { FA_TILE(BMV, NSTV, OCCV, 0) }                                             \
-    else if (lg_spg == 1) { FA_TILE(BMV, NSTV, OCCV, 1) }                                        \
-    else { FA_TILE(BMV, NSTV, OCCV, 2) }
+                           tm, tn, w_scale, x_scale, nsplit, part, tile_cnt);
+// (K splits run only on 128 x 128 tiles, the shape of the few-tile grids)
+#define FA_TILE_2S(LGS, DIR)                                                                     \
+    if (nsplit > 1) { FA_TILE_S(128, 2, 2, LGS, DIR, true) }                                     \
+    else { FA_TILE_S(128, 2, 2, LGS, DIR, false) }
+#define FA_TILE_1(LGS)                                                                           \
+    if (direct) { FA_TILE_S(256, 3, 1, LGS, true, false) }                                       \
+    else { FA_TILE_S(256, 3, 1, LGS, false, false) }
+#define FA_TILE_2(LGS)                                                                           \
+    if (direct) { FA_TILE_2S(LGS, true) }                                                        \
+    else { FA_TILE_2S(LGS, false) }
     if (variant == 1) {
-        FA_TILE_G(256, 3, 1)
+        if (nsplit != 1) return hipErrorInvalidValue;
+        if (lg_spg == 0) { FA_TILE_1(0) }
+        else if (lg_spg == 1) { FA_TILE_1(1) }
+        else { FA_TILE_1(2) }
     } else {
-        FA_TILE_G(128, 2, 2)
+        if (lg_spg == 0) { FA_TILE_2(0) }
+        else if (lg_spg == 1) { FA_TILE_2(1) }
+        else { FA_TILE_2(2) }
     }
-#undef FA_TILE_G
-#undef FA_TILE
-#undef FA_TILE_D
+#undef FA_TILE_1
+#undef FA_TILE_2
+#undef FA_TILE_2S
+#undef FA_TILE_S
     return hipGetLastError();
 }
 

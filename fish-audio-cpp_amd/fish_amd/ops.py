@@ -49,6 +49,12 @@ def w8a8_gemm(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=No
     return Y
 
 
+def k_splits(M, N, K, group_size):
+    """fa_w8a8_gemm_k_splits: 1 when the linear keeps the reference's single
+    group-ordered fp32 chain (bit-exact), else the number of K splits."""
+    return lib().fa_w8a8_gemm_k_splits(M, N, K, group_size)
+
+
 def w8a8_gemm_noalloc(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=None):
     """fa_w8a8_gemm_noalloc: w8a8_gemm with its scratch in the library's
     static per-device array (no device allocation inside the call)."""

@@ -135,6 +135,17 @@ int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_s
                            const int8_t* X_q, const float* X_scale, uint16_t* Y,
                            int M, int N, int K, void* stream);
 
+/* Number of workgroups the linear layer splits K over for this shape (no
+ * reference counterpart): 1 means every output is the reference's single
+ * group-ordered fp32 chain, bit for bit; n > 1 (prefill grids with few tiles,
+ * e.g. 2560 outputs at 512 tokens) means n partial chains over consecutive
+ * whole groups, added in split order: the fp16 output then lies within the
+ * fp32 reassociation bound (1 fp16 ulp + 2^-20 sum_g |term_g * x_scale_g|)
+ * of the reference's, deterministically; the int32 partials are exact either
+ * way.  (16-byte aligned operands assumed; fa_w8a8_gemm_noalloc never
+ * splits.) */
+int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size);
+
 /* Verification hook with no reference counterpart (the reference keeps its
  * int32 partials inside cuBLAS, int8_gemm.cu:476-488): runs exactly the kernel
  * fa_w8a8_gemm_quantized would run for this shape, writes Y, and also writes

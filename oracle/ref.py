@@ -176,6 +176,20 @@ def gemm_quantized(W, w_scale, group_size, xq, xs):
     return Y
 
 
+def split_chain_tolerance(W, w_scale, group_size, xq, xs, y_ref):
+    """Bound on |y - y_ref| for a linear whose fp32 group chain was split into
+    partial chains added afterwards (fa_w8a8_gemm_k_splits > 1): one fp16 ulp
+    of y_ref plus 2^-20 * sum_g |float(P_g) * ws_g * xs_g| (fp32 reassociation
+    of at most 8 partial sums; exact int32 partials).  Returns the bound,
+    [N, M] float64."""
+    W = _c(W, np.int8)
+    P = group_partials(W, xq, group_size).astype(np.float64)        # [N, M, G]
+    ws = np.asarray(w_scale, np.float16).astype(np.float64).reshape(W.shape[0], -1)
+    t = P * ws[None, :, :] * np.asarray(xs, np.float64)[:, None, :]
+    ulp = np.spacing(np.abs(np.asarray(y_ref, np.float16))).astype(np.float64)
+    return ulp + 2.0 ** -20 * np.abs(t).sum(-1)
+
+
 def w8a8_gemm(W, w_scale, group_size, X, act_scale=None, smooth_inv=None):
     W = _c(W, np.int8)
     w_scale = _c(w_scale, np.float16)

@@ -218,6 +218,45 @@ def test_gemm_detects_scale_swap():
         assert_fp16_close(wrong, exact.astype(np.float16), "swapped")
 
 
+@pytest.mark.parametrize("splits", [3, 6, 8])
+def test_split_chain_tolerance(splits):
+    """ref.split_chain_tolerance bounds a K-split group chain: per-split fp32
+    chains (emulated here one rounding per fma in float64 -> float32, over
+    consecutive whole groups), added in split order and rounded to fp16,
+    stay within it of the oracle's single chain; outputs that drop a group
+    or use a neighbouring group's scale fail it."""
+    from fish_amd import synth
+    M, N, K, g = 96, 12, 4096, 256
+    G = K // g
+    q, s = ref.quantize_weights(synth.weights_f16(M, K, seed=5), g)
+    xq, xs = ref.quantize_activations(synth.activations_f16(N, K, seed=6), g)
+    Y = ref.gemm_quantized(q, s, g, xq, xs)
+    P = ref.group_partials(q, xq, g).astype(np.float64)            # [N, M, G]
+    ws = s.astype(np.float32)
+
+    def chain(gs, ge, scale=ws):
+        acc = np.zeros((N, M), np.float32)
+        for gi in range(gs, ge):
+            t = (P[:, :, gi].astype(np.float32) * scale[None, :, gi]).astype(np.float32)
+            acc = (t.astype(np.float64) * xs[:, None, gi] + acc).astype(np.float32)
+        return acc
+
+    bounds = [(G * i) // splits for i in range(splits + 1)]
+    tot = np.zeros((N, M), np.float32)
+    for i in range(splits):
+        tot = (tot + chain(bounds[i], bounds[i + 1])).astype(np.float32)
+    Ys = tot.astype(np.float16)
+    bound = ref.split_chain_tolerance(q, s, g, xq, xs, Y)
+    err = np.abs(Ys.astype(np.float64) - Y.astype(np.float64))
+    assert np.all(err <= bound)
+    assert bound.max() < 0.05 * np.abs(Y.astype(np.float64)).max()
+    # plausible mistakes exceed it
+    dropped = chain(0, G - 1).astype(np.float16)
+    assert np.mean(np.abs(dropped.astype(np.float64) - Y) > bound) > 0.5
+    shifted = chain(0, G, np.roll(ws, 1, axis=1)).astype(np.float16)
+    assert np.mean(np.abs(shifted.astype(np.float64) - Y) > bound) > 0.5
+
+
 # --------------------------------------------------------------- RMSNorm ----
 
 def test_rms_norm_reference_closed_forms():
