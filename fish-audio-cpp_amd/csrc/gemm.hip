@@ -1127,6 +1127,7 @@ int gemm_tile_choice(int M, int N, int K, int g) {
     // g128 always takes 256 x 128.
     if (g == 128) return 1;
     if (g == 64) return 2;
+
     const size_t t256 = (size_t)ceil_div(M, 256) * ceil_div(N, 128);
     return (t256 >= 1024 || (K >= 8192 && t256 >= 128)) ? 1 : 2;
 }
@@ -1140,6 +1141,7 @@ int gemm_tile_split(int M, int N, int K, int g, int variant) {
     // single group-ordered chain (int32 partials stay exact).
     if (variant == 0) variant = gemm_tile_choice(M, N, K, g);
     if (variant != 2 || g < 128) return 1;   // (the g64 split build spills)
+
     const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
     static int cus = 0;
     if (cus == 0) {
@@ -1155,8 +1157,9 @@ int gemm_tile_split(int M, int N, int K, int g, int variant) {
     int sp = slots / tiles;
     if (sp > 8) sp = 8;
     if (sp > units) sp = units;
-    // (measured on MI355X at 512 tokens, g256: o 28.5 -> 24.9 us and down
-    // 61.1 -> 36.3 us at 6 splits; 2 splits made qkv slower, 21.4 -> 27.9 us)
+    // (measured on MI355X at 512 tokens, g256: o 28.5 -> 25.3 us and down
+    // 61.1 -> 36.1 us at 6 splits; 2 splits made qkv slower, 21.4 -> 27.9 us,
+    // and at 2048 tokens 2 to 4 splits made every shape slower)
     return sp < 3 ? 1 : sp;
 }
 

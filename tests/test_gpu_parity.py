@@ -238,21 +238,23 @@ def test_config2_decode_m8_g64_fused_prologue(name):
     assert same(host(xq), rq) and same(host(xs), rs)
     Y, P = ops.w8a8_gemm_partials(dev(q), dev(s), g, xq, xs)
     assert same(host(P), ref.group_partials(q, rq, g))
-    assert same(host(Y), ref.gemm_quantized(q, s, g, rq, rs)), name
+    check_y(host(Y), ref.gemm_quantized(q, s, g, rq, rs), q, s, g, rq, rs,
+            ops.k_splits(Nout, n, K, g))
 
 
 @pytest.mark.parametrize("name", list(LAYER))
 @pytest.mark.parametrize("n,g", [(8, 64), (8, 256), (5, 64), (16, 128), (2, 256)])
-def test_small_batch_linear_bitexact(name, n, g):
-    """2 <= N <= 16 through fa_w8a8_gemm_quantized (the MFMA GEMV with the
-    tokens' codes staged in LDS, which the partials hook does not use): Y
-    bit-identical to the oracle at the configs[2] layer shapes."""
+def test_small_batch_linear(name, n, g):
+    """2 <= N <= 16 through fa_w8a8_gemm_quantized (the MFMA GEMV without
+    the partials hook): Y bit-identical to the oracle at the configs[2] layer
+    shapes (check_y: the GEMV keeps one group chain, k_splits == 1)."""
     K, Nout = LAYER[name]
     q, s = make_linear(Nout, K, g, seed=n + g)
     x = synth.activations_f16(n, K, seed=n + 3)
     rq, rs = ref.quantize_activations(x, g)
     Y = ops.w8a8_gemm_quantized(dev(q), dev(s), g, dev(rq), dev(rs))
-    assert same(host(Y), ref.gemm_quantized(q, s, g, rq, rs)), (name, n, g)
+    check_y(host(Y), ref.gemm_quantized(q, s, g, rq, rs), q, s, g, rq, rs,
+            ops.k_splits(Nout, n, K, g))
 
 
 def test_config3_prefill_m512_qkv_bitexact():
