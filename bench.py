@@ -410,6 +410,7 @@ def run_secondary(torch, ops, st, args):
 
     # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
     out.update(prefill_tops(torch, ops, [(256, 512), (256, 2048), (64, 2048)]))
+    out.update(vendor_int8_gemm(torch))
     out.update(attention_side(torch, ops))
     return out
 
@@ -437,24 +438,48 @@ def attention_side(torch, ops):
     us = graph_us_per_call(
         torch, [lambda: ops.prefill_attention_merged(q, k, v, sc, out=mt)] * 4, reps=5)
     out["prefill_attn_merged_t2048_us"] = round(us, 2)
-    # the DAC transformer's attention (dac_engine.cc:1258-1288): MHA, 16
-    # heads of 64, sliding window 128, here at T = 2048
-    Th, Hh, Dh, Wh = 2048, 16, 64, 128
-    qd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
-    kd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
-    vd = torch.randn((Hh, Th, Dh), generator=gen, device="cuda").half()
-    od = torch.empty_like(qd)
+    # the any-shape kernel (taken for head dims that are not a multiple of 8
+    # or above 128, non-positive scales, or buffers not 16-byte aligned) on
+    # the same shape, here reached through a negative scale
     us = graph_us_per_call(
-        torch, [lambda: ops.prefill_attention(qd, kd, vd, 0.125, window=Wh, out=od)] * 4, reps=5)
-    fl = 4.0 * Dh * Hh * sum(min(i + 1, Wh) for i in range(Th))
-    out["dac_attn_t2048_w128_us"] = round(us, 2)
-    out["dac_attn_t2048_w128_TFLOPs"] = round(fl / (us * 1e-6) / 1e12, 1)
+        torch, [lambda: ops.prefill_attention(q, k, v, -sc, out=o)], reps=1, rounds=3)
+    out["prefill_attn_anyshape_t2048_us"] = round(us, 1)
     us = graph_us_per_call(torch, [lambda: ops.qkv_split_heads_gqa(qkv, n_q, n_kv, D)] * 4)
     out["qkv_split_t2048_us"] = round(us, 2)
     out["qkv_split_t2048_GBs"] = round(2 * qkv.numel() * 2 / (us * 1e-6) / 1e9, 1)
     us = graph_us_per_call(torch, [lambda: ops.merge_heads(o, out=m)] * 4)
     out["merge_heads_t2048_us"] = round(us, 2)
     out["merge_heads_t2048_GBs"] = round(2 * o.numel() * 2 / (us * 1e-6) / 1e9, 1)
+    return out
+
+
+def vendor_int8_gemm(torch):
+    """Context for configs[3]: the vendor library's plain int8 GEMM
+    (torch._int_mm, int8 x int8 -> int32, no group scales, no epilogue) on
+    the same four layer shapes at 2048 tokens, random operands, timed the
+    same way.  Not part of the product; a yardstick for the MFMA roofline
+    these shapes reach on this device."""
+    from fish_amd.synth import LAYER_SHAPES
+    out = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    M = 2048
+    tot_ops, tot_us = 0.0, 0.0
+    for name, (K, N) in LAYER_SHAPES.items():
+        a = torch.randint(-127, 128, (M, K), generator=gen, device="cuda", dtype=torch.int8)
+        b = torch.randint(-127, 128, (N, K), generator=gen, device="cuda", dtype=torch.int8)
+        bt = b.t()
+        try:
+            us = graph_us_per_call(torch, [lambda: torch._int_mm(a, bt)] * 8, reps=5)
+        except Exception as e:   # the library may not take a shape
+            out["vendor_int8_mm_m2048_%s" % name] = "unavailable: %s" % str(e)[:80]
+            continue
+        o = 2.0 * M * N * K
+        tot_ops += o
+        tot_us += us
+        out["vendor_int8_mm_m2048_%s_TOPS" % name] = round(o / (us * 1e-6) / 1e12, 1)
+    if tot_us > 0:
+        out["vendor_int8_mm_m2048_layer_TOPS"] = round(tot_ops / (tot_us * 1e-6) / 1e12, 1)
     return out
 
 
