@@ -72,6 +72,24 @@ def test_chain_stack_bitexact(g):
     assert same(h_stack, stack_oracle(st, host(st.h0), g))
 
 
+def test_stack_and_chain_36_layers():
+    """configs[4] at its full size: 36 layers of distinct weights, one token,
+    g256 -- the four-launch stack, the chain launch and the oracle's chain
+    of separate functions end in the same residual stream, bit for bit."""
+    from fish_amd.decode_stack import DecodeStack
+    st = DecodeStack(n_layers=36, g=256, tokens=1, seed=23)
+    st.h.copy_(st.h0)
+    st.run_stack()
+    h_stack = host(st.h).copy()
+    st.h.copy_(st.h0)
+    st.run_chain()
+    assert same(host(st.h), h_stack), "chain != stack at 36 layers"
+    st.chain.close()
+    h_ref = stack_oracle(st, host(st.h0), 256)
+    assert same(h_stack, h_ref), "stack != oracle at 36 layers"
+    assert np.isfinite(h_ref.astype(np.float32)).all()
+
+
 @pytest.mark.parametrize("g", [64, 128, 256])
 def test_chain_step_kinds_bitexact(g):
     """Every step kind, odd row counts, and a step reading what an earlier
