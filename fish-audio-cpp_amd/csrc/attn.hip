@@ -340,64 +340,114 @@ attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
 
 // Any-shape attention (head dim not a multiple of 8 or above 128, a
 // non-positive scale, or buffers not 16-byte aligned): one wave per (query
-// head, query), three passes over the query's visible keys, in the
-// reference's order of operations -- the row max of the fp16-rounded, scaled
-// scores; their exp-sum; then P = fp16(exp(v - max) * (1 / sum)) and
-// O[d] = fp16(sum_j float(P_j) * float(V_jd)) with the fma chain in key order
-// (causal_softmax_kernel and sgemv_kernel, prefill_attention.cu:141-224,
-// 325-349).  Lanes take keys for the scores and head-dim columns for O.
-// Correct for every shape the API accepts; not a fast path.
+// head, query), two passes over the query's visible keys in blocks of 64,
+// with the reference's operations (causal_softmax_kernel and sgemv_kernel,
+// prefill_attention.cu:141-224, 325-349): scores float(fp16(q . k_j)) *
+// scale; their max and exp-sum (one pass, the sum rescaled when the running
+// max grows); then P = fp16(exp(v - max) * (1 / sum)) and
+// O[d] = fp16(sum_j float(P_j) * float(V_jd)) with the fma chain in key order.
+// A block's key rows are copied into the wave's LDS area 64 head-dim columns
+// at a time with consecutive addresses (2-byte loads: any alignment), and
+// lane j forms key j's dot product from there (rows padded to 66 halves, so
+// the 64 lanes' reads fall in distinct banks); for O the lanes take head-dim
+// columns of each V row.  Correct for every shape the API accepts; a
+// fallback, not a fast path.
 constexpr int kGenMaxD = 512;
+constexpr int kGenRow = 66;      // LDS row stride of a staged key block (halves)
 
 __global__ void __launch_bounds__(256)
 attention_generic_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                          const uint16_t* __restrict__ v, uint16_t* __restrict__ out, int n_q,
                          int n_kv, int T, int D, float sm_scale, int window, bool token_major) {
+    __shared__ uint16_t kblk[4][64 * kGenRow];
+    __shared__ uint16_t qrow[4][kGenMaxD];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t idx = (int64_t)blockIdx.x * 4 + wave;
-    if (idx >= (int64_t)n_q * T) return;          // whole wave; no barriers below
+    if (idx >= (int64_t)n_q * T) return;          // whole wave; only wave-local LDS below
     const int head = (int)(idx / T), i = (int)(idx % T);
     const int g = head / (n_q / n_kv);
     const uint16_t* qr = q + ((int64_t)head * T + i) * D;
     const uint16_t* Kg = k + (int64_t)g * T * D;
     const uint16_t* Vg = v + (int64_t)g * T * D;
     const int left = window > 0 ? max(0, i - window + 1) : 0;
-    auto score = [&](int j) {        // float(fp16(q . k_j)) * sm_scale
-        const uint16_t* kr = Kg + (int64_t)j * D;
+    uint16_t* kb = kblk[wave];
+    uint16_t* qs = qrow[wave];
+    for (int d = lane; d < D; d += 64) qs[d] = qr[d];
+    // lane's score float(fp16(q . k_{j0 + lane})) * scale for the block at
+    // j0 (rows past i read row i; their scores are not used).  A wave reads
+    // back only LDS it wrote itself, in order: no barrier, only a wait.
+    auto block_scores = [&](int j0) {
         float acc = 0.0f;
-        for (int d = 0; d < D; ++d) acc = __builtin_fmaf(h2f(qr[d]), h2f(kr[d]), acc);
+        for (int c0 = 0; c0 < D; c0 += 64) {
+            const int cw = min(64, D - c0);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // earlier reads done
+            const int cl = min(lane, cw - 1);
+            for (int r0 = 0; r0 < 64; r0 += 16) {
+                uint16_t kv[16];          // 16 loads in flight, then the writes
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    kv[r] = Kg[(int64_t)min(j0 + r0 + r, i) * D + c0 + cl];
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (lane < cw) kb[(r0 + r) * kGenRow + lane] = kv[r];
+            }
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            const uint16_t* row = kb + lane * kGenRow;
+#pragma unroll 8
+            for (int c = 0; c < cw; ++c)
+                acc = __builtin_fmaf(h2f(qs[c0 + c]), h2f(row[c]), acc);
+        }
         return h2f(f2h(acc)) * sm_scale;
     };
-    float mx = -__builtin_inff();
-    for (int j = left + lane; j <= i; j += 64) mx = fmaxf(mx, score(j));
-    mx = subgroup_max<64>(mx);
-    float sum = 0.0f;
-    for (int j = left + lane; j <= i; j += 64) sum += expf(score(j) - mx);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    float o[kGenMaxD / 64];
-#pragma unroll
-    for (int r = 0; r < kGenMaxD / 64; ++r) o[r] = 0.0f;
+    // pass 1: running max and exp-sum over blocks (per block: its max, then
+    // the sum rescaled to it)
+    float m = -__builtin_inff(), l = 0.0f;
     for (int j0 = left; j0 <= i; j0 += 64) {
-        const int j = j0 + lane;
-        const float p = j <= i ? h2f(f2h(expf(score(j) - mx) * inv)) : 0.0f;
-        const int nj = min(64, i - j0 + 1);
-        for (int t = 0; t < nj; ++t) {       // t is wave-uniform: a lane read
-            const float pj =
-                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), t));
-            const uint16_t* vr = Vg + (int64_t)(j0 + t) * D;
+        const bool ok = j0 + lane <= i;
+        const float s = block_scores(j0);
+        const float bm = subgroup_max<64>(ok ? s : -__builtin_inff());
+        const float mn = fmaxf(m, bm);
+        float e = ok ? expf(s - mn) : 0.0f;
 #pragma unroll
-            for (int r = 0; r < kGenMaxD / 64; ++r) {
+        for (int off = 32; off > 0; off >>= 1) e += __shfl_xor(e, off, 64);
+        l = (m == mn ? l : l * expf(m - mn)) + e;
+        m = mn;
+    }
+    const float mx = m;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // pass 2: P and the key-ordered O chains
+    constexpr int QR = kGenMaxD / 64;
+    float o[QR];
+#pragma unroll
+    for (int r = 0; r < QR; ++r) o[r] = 0.0f;
+    for (int j0 = left; j0 <= i; j0 += 64) {
+        const float s = block_scores(j0);
+        const float p = j0 + lane <= i ? h2f(f2h(expf(s - mx) * inv)) : 0.0f;
+        const int nj = min(64, i - j0 + 1);
+        // eight keys' V values in flight at a time (keys past i have P = 0
+        // and read row i)
+        for (int t0 = 0; t0 < nj; t0 += 8) {
+#pragma unroll
+            for (int r = 0; r < QR; ++r) {
+                if (r * 64 >= D) continue;    // wave-uniform
                 const int d = lane + 64 * r;
-                if (d < D) o[r] = __builtin_fmaf(pj, h2f(vr[d]), o[r]);
+                const int dc = d < D ? d : D - 1;
+                uint16_t vv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) vv[u] = Vg[(int64_t)min(j0 + t0 + u, i) * D + dc];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const float pj = __builtin_bit_cast(   // t0 + u is wave-uniform: a lane read
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), t0 + u));
+                    o[r] = __builtin_fmaf(pj, h2f(vv[u]), o[r]);
+                }
             }
         }
     }
     uint16_t* orow = out + (token_major ? ((int64_t)i * n_q + head) * D
                                         : ((int64_t)head * T + i) * D);
 #pragma unroll
-    for (int r = 0; r < kGenMaxD / 64; ++r) {
+    for (int r = 0; r < QR; ++r) {
         const int d = lane + 64 * r;
         if (d < D) orow[d] = f2h(o[r]);
     }
