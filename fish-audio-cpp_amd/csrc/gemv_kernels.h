@@ -619,9 +619,23 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
         __syncthreads();
         for (int t = threadIdx.x; t < kTile * N; t += blockDim.x) {
             const int r = t & (kTile - 1), tok = t >> 4;
+            const float* tp = tl + tok * kTile + r;      // term of group gi at gi * ns * kTile
+            const float* xp = xs_s + tok * G;
             float acc = 0.0f;
-            for (int gi = 0; gi < G; ++gi)
-                acc = __builtin_fmaf(tl[(gi * ns + tok) * kTile + r], xs_s[tok * G + gi], acc);
+            // eight groups' operands read before their eight fmas, so the
+            // chain waits on LDS once per eight groups, not once per group
+            int gi = 0;
+            for (; gi + 8 <= G; gi += 8) {
+                float tv[8], xv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    tv[u] = tp[(gi + u) * ns * kTile];
+                    xv[u] = xp[gi + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(tv[u], xv[u], acc);
+            }
+            for (; gi < G; ++gi) acc = __builtin_fmaf(tp[gi * ns * kTile], xp[gi], acc);
             if (row0 + r < M) Y[(size_t)tok * M + row0 + r] = f2h(acc);
         }
     } else {
