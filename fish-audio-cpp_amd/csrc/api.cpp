@@ -15,8 +15,12 @@
 #include "chain.h"
 #include "../../include/fish_w8a8.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -170,6 +174,136 @@ bool overlaps(const uint16_t* a, size_t n, const uint16_t* b, size_t m) {
     return a && b && a < b + m && b < a + n;
 }
 
+// ---------------------------------------------------- per-shape timing ----
+//
+// The reference's FISH_INT8_PROFILE (src/kernels/int8_gemm.cu:45-145,
+// 398-510): with the variable set to a non-empty value other than "0" (or
+// after fa_profile_enable(1)), each call of the linear entry points is timed
+// with events on its stream, waited for, and added to a bucket keyed by
+// entry, shape, group size and quantization mode; the buckets are printed
+// to stderr at exit and can be read with fa_profile_summary.  Calls on a
+// stream under graph capture are not timed (waiting is not allowed there),
+// and an entry point called from another one is timed once, as the outer
+// call.
+
+struct ProfBucket {
+    uint64_t calls = 0;
+    uint64_t groups = 0;
+    double total_ms = 0.0, quant_ms = 0.0, linear_ms = 0.0;
+};
+
+struct ProfState {
+    std::mutex mu;
+    std::map<std::string, ProfBucket> buckets;
+    std::string summary() {
+        std::lock_guard<std::mutex> lock(mu);
+        if (buckets.empty()) return std::string();
+        std::string out = "INT8 profile summary:\n";
+        char line[512];
+        for (const auto& kv : buckets) {
+            const ProfBucket& b = kv.second;
+            const double c = b.calls ? (double)b.calls : 1.0;
+            snprintf(line, sizeof line,
+                     "  %s calls=%llu avg_groups=%.1f total=%.3fms avg=%.3fms "
+                     "(quant=%.3f gemm=%.3f)\n",
+                     kv.first.c_str(), (unsigned long long)b.calls, (double)b.groups / c,
+                     b.total_ms, b.total_ms / c, b.quant_ms / c, b.linear_ms / c);
+            out += line;
+        }
+        return out;
+    }
+    ~ProfState() {   // host data only: no device call at exit
+        const std::string t = summary();
+        if (!t.empty()) fputs(t.c_str(), stderr);
+    }
+};
+
+ProfState& prof_state() {
+    static ProfState state;
+    return state;
+}
+
+std::atomic<int> g_prof_on{-1};   // -1: not yet read from the environment
+
+bool prof_enabled() {
+    int v = g_prof_on.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char* e = std::getenv("FISH_INT8_PROFILE");
+        v = (e && *e && std::string(e) != "0") ? 1 : 0;
+        int expect = -1;
+        g_prof_on.compare_exchange_strong(expect, v);
+        v = g_prof_on.load(std::memory_order_relaxed);
+    }
+    return v > 0;
+}
+
+struct ProfEvents {
+    hipEvent_t e[3] = {nullptr, nullptr, nullptr};
+};
+thread_local std::unordered_map<int, ProfEvents> t_prof_ev;   // per device
+thread_local int t_prof_depth = 0;
+
+class ProfCall;
+thread_local ProfCall* t_prof = nullptr;
+
+class ProfCall {
+  public:
+    explicit ProfCall(void* stream) : s_((hipStream_t)stream) {
+        if (t_prof_depth++ > 0 || !prof_enabled()) return;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s_, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return;
+        ProfEvents& pe = t_prof_ev[dev];
+        for (auto& e : pe.e)
+            if (!e && hipEventCreate(&e) != hipSuccess) return;
+        if (hipEventRecord(pe.e[0], s_) != hipSuccess) return;
+        ev_ = &pe;
+        t_prof = this;
+    }
+    ~ProfCall() {
+        --t_prof_depth;
+        if (t_prof == this) t_prof = nullptr;
+    }
+    ProfCall(const ProfCall&) = delete;
+    ProfCall& operator=(const ProfCall&) = delete;
+    // end of the quantization phase (a separate launch before the linear)
+    void mark() {
+        if (ev_ && !marked_ && hipEventRecord(ev_->e[1], s_) == hipSuccess) marked_ = true;
+    }
+    void finish(const char* entry, int M, int N, int K, int group_size, bool static_act,
+                bool smooth) {
+        if (!ev_) return;
+        float total = 0.0f, quant = 0.0f;
+        if (hipEventRecord(ev_->e[2], s_) != hipSuccess || hipEventSynchronize(ev_->e[2]) != hipSuccess ||
+            hipEventElapsedTime(&total, ev_->e[0], ev_->e[2]) != hipSuccess)
+            return;
+        if (marked_ && hipEventElapsedTime(&quant, ev_->e[0], ev_->e[1]) != hipSuccess) quant = 0.0f;
+        const int g = eff_group(K, group_size);
+        char key[256];
+        snprintf(key, sizeof key, "%s M=%d N=%d K=%d group=%d act=%s smooth=%s", entry, M, N, K, g,
+                 static_act ? "static" : "dynamic", smooth ? "yes" : "no");
+        ProfState& ps = prof_state();
+        std::lock_guard<std::mutex> lock(ps.mu);
+        ProfBucket& b = ps.buckets[key];
+        b.calls += 1;
+        b.groups += (uint64_t)((K + g - 1) / g);
+        b.total_ms += total;
+        b.quant_ms += quant;
+        b.linear_ms += total - quant;
+    }
+
+  private:
+    hipStream_t s_;
+    ProfEvents* ev_ = nullptr;
+    bool marked_ = false;
+};
+
+// Called by an entry point between its quantization launch and its linear.
+void prof_mark() {
+    if (t_prof) t_prof->mark();
+}
+
 }  // namespace
 
 namespace fa {
@@ -226,7 +360,7 @@ int fa_w8a8_gemm_partials(const int8_t* W, const uint16_t* w_scale, int group_si
                             toks, M, N, K, (hipStream_t)stream);
 }
 
-int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
+static int gemm_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
                  const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* X,
                  uint16_t* Y, int M, int N, int K, void* stream) {
     const char* fn = "fa_w8a8_gemm";
@@ -262,8 +396,19 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
     if (rc) return rc;
     FA_HIP(fa::launch_quantize_activations(X, nullptr, fa::Prologue::kPlain, act_scale, smooth_inv,
                                            ws->xq, ws->xs, nullptr, N, K, g, G, s));
+    prof_mark();
     return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             s);
+}
+
+int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
+                 const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* X,
+                 uint16_t* Y, int M, int N, int K, void* stream) {
+    ProfCall pc(stream);
+    const int rc = gemm_impl(W, w_scale, group_size, act_scale, smooth_inv, X, Y, M, N, K, stream);
+    if (rc == FA_OK && M > 0 && N > 0)
+        pc.finish("fa_w8a8_gemm", M, N, K, group_size, act_scale, smooth_inv);
+    return rc;
 }
 
 // ------------------------------------------------- no-alloc variant ----
@@ -357,7 +502,7 @@ int fa_w8a8_gemm_noalloc(const int8_t* W, const uint16_t* w_scale, int group_siz
                             tables);
 }
 
-int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
+static int gemm_rms_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
                      const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
                      const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
                      uint16_t* Y, int M, int N, int K, void* stream) {
@@ -416,7 +561,7 @@ int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
                             s);
 }
 
-int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_size,
+static int gemm_swiglu_impl(const int8_t* W13, const uint16_t* w13_scale, int group_size,
                         const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
                         const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
                         uint16_t* act, int F, int N, int K, void* stream) {
@@ -474,7 +619,7 @@ int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_
     return FA_OK;
 }
 
-int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_size,
+static int gemm_silu_mul_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
                           const uint16_t* act_scale, const uint16_t* smooth_inv,
                           const uint16_t* gate, const uint16_t* up, uint16_t* Y, int M, int N,
                           int K, void* stream) {
@@ -513,6 +658,64 @@ int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_si
                                            ws->xq, ws->xs, nullptr, N, K, g, G, s));
     return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             s);
+}
+
+int fa_w8a8_gemm_rms(const int8_t* W, const uint16_t* w_scale, int group_size,
+                     const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
+                     const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
+                     uint16_t* Y, int M, int N, int K, void* stream) {
+    ProfCall pc(stream);
+    const int rc = gemm_rms_impl(W, w_scale, group_size, act_scale, smooth_inv, x, resid, h_out,
+                                 gamma, eps, Y, M, N, K, stream);
+    if (rc == FA_OK && M > 0 && N > 0)
+        pc.finish("fa_w8a8_gemm_rms", M, N, K, group_size, act_scale, smooth_inv);
+    return rc;
+}
+
+int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_size,
+                        const uint16_t* act_scale, const uint16_t* smooth_inv, const uint16_t* x,
+                        const uint16_t* resid, uint16_t* h_out, const uint16_t* gamma, float eps,
+                        uint16_t* act, int F, int N, int K, void* stream) {
+    ProfCall pc(stream);
+    const int rc = gemm_swiglu_impl(W13, w13_scale, group_size, act_scale, smooth_inv, x, resid,
+                                    h_out, gamma, eps, act, F, N, K, stream);
+    if (rc == FA_OK && F > 0 && N > 0)
+        pc.finish("fa_w8a8_gemm_swiglu", 2 * F, N, K, group_size, act_scale, smooth_inv);
+    return rc;
+}
+
+int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_size,
+                          const uint16_t* act_scale, const uint16_t* smooth_inv,
+                          const uint16_t* gate, const uint16_t* up, uint16_t* Y, int M, int N,
+                          int K, void* stream) {
+    ProfCall pc(stream);
+    const int rc = gemm_silu_mul_impl(W, w_scale, group_size, act_scale, smooth_inv, gate, up, Y,
+                                      M, N, K, stream);
+    if (rc == FA_OK && M > 0 && N > 0)
+        pc.finish("fa_w8a8_gemm_silu_mul", M, N, K, group_size, act_scale, smooth_inv);
+    return rc;
+}
+
+int fa_profile_enable(int on) {
+    const int prev = prof_enabled() ? 1 : 0;
+    g_prof_on.store(on ? 1 : 0, std::memory_order_relaxed);
+    return prev;
+}
+
+size_t fa_profile_summary(char* buf, size_t n) {
+    const std::string t = prof_state().summary();
+    if (buf && n > 0) {
+        const size_t c = t.size() < n - 1 ? t.size() : n - 1;
+        memcpy(buf, t.data(), c);
+        buf[c] = 0;
+    }
+    return t.size();
+}
+
+void fa_profile_reset(void) {
+    ProfState& ps = prof_state();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    ps.buckets.clear();
 }
 
 int fa_gemm_fp16(const uint16_t* W, const uint16_t* X, uint16_t* Y, int M, int N, int K,

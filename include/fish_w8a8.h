@@ -320,6 +320,26 @@ int fa_workspace_reserve(int max_tokens, int max_M, int max_K, int min_group_siz
 int fa_workspace_release(void);
 
 /* ------------------------------------------------------------------------ */
+/* Per-shape timing (src/kernels/int8_gemm.cu:45-145, FISH_INT8_PROFILE).    */
+/* ------------------------------------------------------------------------ */
+
+/* With FISH_INT8_PROFILE set to a non-empty value other than "0", or after
+ * fa_profile_enable(1), each call of fa_w8a8_gemm, fa_w8a8_gemm_rms,
+ * fa_w8a8_gemm_swiglu and fa_w8a8_gemm_silu_mul is timed with events on its
+ * stream and waited for (so profiling serialises the caller, as the
+ * reference's does); times accumulate per (entry, M, N, K, group size,
+ * static / dynamic activation scales, smooth_inv) and are printed to stderr
+ * at process exit, as "quant" (a separate quantization launch) and "gemm"
+ * (everything else).  Calls on a stream under graph capture are not timed.
+ * fa_profile_enable returns the previous setting. */
+int fa_profile_enable(int on);
+/* Copies the summary text (at most n - 1 bytes and a NUL) into buf and
+ * returns its full length; buf may be NULL to query the length. */
+size_t fa_profile_summary(char* buf, size_t n);
+/* Clears the accumulated times. */
+void fa_profile_reset(void);
+
+/* ------------------------------------------------------------------------ */
 /* dual_ar.bin container (src/model/tensor.h:8-67, src/model/loader.cc).     */
 /* ------------------------------------------------------------------------ */
 
