@@ -351,6 +351,22 @@ def run_secondary(torch, ops, st, args):
                                      "GB/s": round(sa.awq_stack_bytes() / t / 1e9, 1)}
     del sa, g_awq
     torch.cuda.empty_cache()
+    # configs[4] at g64 (4x the scale bytes)
+    s64 = DecodeStack(n_layers=args.layers, g=64, tokens=1, seed=9)
+    s64.h.copy_(s64.h0)
+    g_64 = s64.capture(lambda: s64.run_stack())
+    for _ in range(2):
+        g_64.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_64.replay()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    out["cfg4_stack_g64_m1"] = {"step_ms": round(t * 1e3, 4),
+                                "GB/s": round(s64.stack_bytes() / t / 1e9, 1)}
+    del s64, g_64
+    torch.cuda.empty_cache()
     # the fast (codebook) decoder: 4 layers + int8 head (4096 x 2560), 10
     # passes per frame over the same ~0.4 GB of weights
     from fish_amd.decode_stack import FastDecoder, NUM_CODEBOOKS
