@@ -258,7 +258,8 @@ __global__ __launch_bounds__(NTH, 1) void chain_kernel(const ChainStepDev* __res
         while (u.s < nsteps && u.rem == 0) start(u, u.s + 1);
     };
     // this lane's weight and scale-pair addresses of item u (rows past M
-    // read row M - 1; bytes past K read the row start: both never used)
+    // read row M - 1, bytes past K the row start; such rows are never
+    // stored and such bytes' products are dropped)
     auto item_addr = [&](const Cursor& u, const int8_t*& wp, const uint16_t*& sp) {
         int row = 2 * (u.pa + u.pl) + rsub;
         row = row < u.c.M ? row : u.c.M - 1;
@@ -570,6 +571,8 @@ __global__ __launch_bounds__(NTH, 1) void chain_kernel(const ChainStepDev* __res
                 p = __builtin_amdgcn_sdot4(wv.y, xq.y, p, false);
                 p = __builtin_amdgcn_sdot4(wv.z, xq.z, p, false);
                 p = __builtin_amdgcn_sdot4(wv.w, xq.w, p, false);
+                // bytes past K (a short last group) add nothing to its sum
+                p = live ? p : 0;
                 p = lane_group_sum<LG>(p);
                 int row = 2 * (cs.pa + pl) + rsub;
                 row = row < cs.c.M ? row : cs.c.M - 1;

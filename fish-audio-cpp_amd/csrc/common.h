@@ -125,6 +125,10 @@ hipError_t launch_quantize_weights(const uint16_t* w, int64_t rows, int64_t K, i
 
 // Decode GEMV (N <= 16 tokens): a v_dot4 kernel for N == 1 and an int8 MFMA
 // kernel for 2 <= N <= 16.  kind == 0 means "shape not taken".
+// Compute units of the current device (0 if the query fails); cached per
+// device.
+int device_cus();
+
 struct GemvPlan {
     int kind = 0;    // 1, 2: dot kernel with 1 or 2 rows per wave; 3: MFMA kernel
                      // (dot: grid = row blocks)

@@ -158,7 +158,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(
                     P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], P[i][j], 0, 0, 0);
         }
 
-        if (++sig == spg) {
+        // (a short last group, K % g != 0, ends with the last step)
+        if (++sig == spg || step + 1 == nsteps) {
             const int sb = gi & 1;
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -482,7 +483,8 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
                     }
                 }
                 const int tcur = s * KS + q;
-                if ((kAb & 4) == 0 && ((tcur + 1) & spg_m1) == 0) {
+                // a group ends with its last substep, or (K % g != 0) with K
+                if ((kAb & 4) == 0 && (((tcur + 1) & spg_m1) == 0 || tcur + 1 == nsub)) {
                     const int gi = tcur >> lg_spg;
                     const int sl = gi & 3;
 #pragma unroll
@@ -1143,14 +1145,8 @@ int gemm_tile_split(int M, int N, int K, int g, int variant) {
     if (variant != 2 || g < 128) return 1;   // (the g64 split build spills)
 
     const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return 1;
-        cus = n;
-    }
+    const int cus = device_cus();
+    if (cus <= 0) return 1;
     const int slots = cus * 2;   // two 128 x 128 workgroups per CU
     if (tiles * 2 > slots) return 1;
     const int units = (K / 128) / (g >= 256 ? g / 128 : 1);

@@ -4,6 +4,8 @@
 // instantiated in gemv_dot*.hip.
 #include "gemv_kernels.h"
 
+#include <atomic>
+
 namespace fa {
 using namespace gv;
 namespace {
@@ -49,21 +51,20 @@ int round_maxg(int m) {
     return 20;
 }
 
-// Compute units of the current device (cached per device).
+}  // namespace
+
 int device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64];   // zero-initialised (static storage)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
-
-}  // namespace
 
 GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi) {
     GemvPlan p{};

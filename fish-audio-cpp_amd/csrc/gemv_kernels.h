@@ -518,6 +518,10 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int gb = (wave * G) / NW;
     const int ng = ((wave + 1) * G) / NW - gb;
     const int nsteps = ng * SPG;
+    // steps of the wave's range that lie inside the row: when K % g != 0 the
+    // last group is short (K % 64 == 0 here); later steps re-load step 0
+    // (in bounds) and skip their MFMA
+    const int nvalid = min(nsteps, (K - gb * SPG * 64) / 64);
 
     const int lr = lane & 15;            // A: weight row in tile; B: token
     const int kq = (lane >> 4) * 16;
@@ -539,12 +543,12 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     if constexpr (BH) {
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st)
-            bh[st] = ld16(xp + (size_t)(st < nsteps ? st : 0) * 64);
+            bh[st] = ld16(xp + (size_t)(st < nvalid ? st : 0) * 64);
     }
     // unconditional loads, no select on the loaded data: a select would make
     // the compiler wait for each load right where it is issued
     auto load = [&](int slot, int step) {
-        const size_t off = (size_t)(step < nsteps ? step : 0) * 64;
+        const size_t off = (size_t)(step < nvalid ? step : 0) * 64;
         a[slot] = ld16(wp + off);
         if constexpr (BH) {
         } else if constexpr ((kAb & 1) == 0) b[slot] = ld16(xp + off);
@@ -586,10 +590,12 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
         for (int s = 0; s < SPG; ++s) {
             const int step = j * SPG + s;
             const int slot = step % KD;
-            if constexpr (BH)
-                P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], bh[step], P, 0, 0, 0);
-            else
-                P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], b[slot], P, 0, 0, 0);
+            if (step < nvalid) {   // wave-uniform
+                if constexpr (BH)
+                    P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], bh[step], P, 0, 0, 0);
+                else
+                    P = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[slot], b[slot], P, 0, 0, 0);
+            }
             load(slot, step + KD);
         }
         const int gi = gb + (j < ng ? j : 0);

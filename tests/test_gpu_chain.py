@@ -90,12 +90,14 @@ def test_stack_and_chain_36_layers():
     assert np.isfinite(h_ref.astype(np.float32)).all()
 
 
+@pytest.mark.parametrize("ks", [(512, 768, 1024), (528, 784, 1040)])
 @pytest.mark.parametrize("g", [64, 128, 256])
-def test_chain_step_kinds_bitexact(g):
+def test_chain_step_kinds_bitexact(g, ks):
     """Every step kind, odd row counts, and a step reading what an earlier
-    step's prologue wrote (h_out), against the oracle."""
+    step's prologue wrote (h_out), against the oracle; the second K set
+    leaves every step's last group short (K % g != 0)."""
     rng = np.random.default_rng(100 + g)
-    K0, K1, K2 = 512, 768, 1024
+    K0, K1, K2 = ks
     W0, s0 = ref.quantize_weights(synth.weights_f16(37, K0, seed=1), g)
     W1, s1 = ref.quantize_weights(synth.weights_f16(70, K1, seed=2), g)
     W2, s2 = ref.quantize_weights(synth.weights_f16(2 * 33, K2, seed=3), g)

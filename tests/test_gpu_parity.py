@@ -328,11 +328,41 @@ def test_prefill_k_split_512_tokens(name):
     (33, 64, 384, 128),     # K % 256 == 128: pipelined kernel, odd stage count
     (70, 259, 768, 256),    # tile kernel, in-kernel scale gather, M * G odd (last pair clamped)
     (40, 333, 256, 256),    # one group: 1-D scales, M odd
+    (9, 389, 3392, 128),    # MFMA GEMV, K % g != 0: the last group one 64-byte step
+    (5, 100, 192, 128),     # MFMA GEMV, two groups, the second short
+    (16, 77, 1344, 256),    # MFMA GEMV, g256, last group 64 of 256 bytes
+    (40, 300, 640, 512),    # pipelined kernel, g512, last group 128 bytes
     (3, 40, 100, 48),       # K, g not multiples of 64: generic kernel
     (20, 33, 96, 32),       # generic kernel, N > 16
 ])
 def test_edge_shapes(N, M, K, g):
     check_linear(N, M, K, g, seed=N + M)
+
+
+def _sweep_shapes(n=28, seed=2024):
+    """Seeded random (N, M, K, g): one-token, small-batch and GEMM token
+    counts, row counts that leave every tile ragged, K a multiple of 16 (and
+    a few that are not), every group size the paths take."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        N = int(rng.choice([1, int(rng.integers(2, 17)), int(rng.integers(17, 129)),
+                            int(rng.integers(129, 700))]))
+        M = int(rng.integers(1, 3000))
+        g = int(rng.choice([64, 128, 256, 512, 0]))
+        K = int(rng.integers(1, 257)) * 16 if rng.random() < 0.85 else int(rng.integers(8, 2500))
+        if N * M * K > 1.5e9:
+            continue
+        out.append((N, M, K, g))
+    return out
+
+
+@pytest.mark.parametrize("N,M,K,g", _sweep_shapes())
+def test_random_shape_sweep(N, M, K, g):
+    """Partials bit-exact and Y as the oracle's on seeded random shapes,
+    through the partials hook and the full entry point."""
+    print("sweep N=%d M=%d K=%d g=%d" % (N, M, K, g), flush=True)
+    check_linear(N, M, K, g, seed=(N * 7 + M * 3 + K) % 1000)
 
 
 def test_unaligned_weight_uses_exact_path():
@@ -526,6 +556,67 @@ def test_gemm_swiglu_bitexact(g, T, mode):
     up = ref.gemm_quantized(q3, s3, g, rq, rs)
     _, _, ract = ref.silu_mul_quant(gate, up, g)
     assert same(host(act), ract)
+
+
+def _fused_sweep(n=18, seed=77):
+    """Seeded random cases for the fused entry points: (entry, T, M, K, g)."""
+    rng = np.random.default_rng(seed)
+    entries = ["rms", "rms_resid", "silu_mul", "swiglu", "swiglu_rms"]
+    out = []
+    for i in range(n):
+        e = entries[i % len(entries)]
+        T = int(rng.choice([1, 1, 2, int(rng.integers(3, 40))]))
+        M = int(rng.integers(1, 1500)) * (2 if e.startswith("swiglu") else 1)
+        K = int(rng.integers(1, 400)) * 16
+        g = int(rng.choice([64, 128, 256, 512]))
+        out.append((e, T, M, K, g))
+    return out
+
+
+@pytest.mark.parametrize("entry,T,M,K,g", _fused_sweep())
+def test_fused_entry_sweep(entry, T, M, K, g):
+    """The fused entry points on seeded random shapes (K % g often nonzero,
+    odd row counts), against the oracle's chain of separate functions."""
+    print("fused %s T=%d M=%d K=%d g=%d" % (entry, T, M, K, g), flush=True)
+    rng = np.random.default_rng(M * 31 + K)
+    x = synth.activations_f16(T, K, seed=M)
+    gam = synth.gamma_f16(K, seed=K)
+    res = synth.activations_f16(T, K, seed=M + 1)
+    if entry.startswith("swiglu"):
+        F = M // 2
+        q1, s1 = make_linear(F, K, g, seed=M + 2)
+        q3, s3 = make_linear(F, K, g, seed=M + 3)
+        q13 = np.stack((q1, q3), axis=1).reshape(2 * F, K)
+        s13 = np.stack((s1, s3), axis=1).reshape(2 * F, -1)
+        if entry == "swiglu":
+            act = ops.w8a8_gemm_swiglu(dev(q13), dev(s13), dev(x), g)
+            rq, rs = ref.quantize_activations(x, g)
+        else:
+            h_out = torch.empty((T, K), dtype=torch.float16, device="cuda")
+            act = ops.w8a8_gemm_swiglu(dev(q13), dev(s13), dev(x), g, gamma=dev(gam), eps=1e-6,
+                                       resid=dev(res), h_out=h_out)
+            h = ref.residual_add(x, res)
+            rq, rs, _ = ref.rms_norm_quant(h, gam, 1e-6, g)
+            assert same(host(h_out), h)
+        _, _, ract = ref.silu_mul_quant(ref.gemm_quantized(q1, s1, g, rq, rs),
+                                        ref.gemm_quantized(q3, s3, g, rq, rs), g)
+        assert same(host(act), ract)
+        return
+    q, s_ = make_linear(M, K, g, seed=M + 4)
+    if entry == "silu_mul":
+        gate = (rng.standard_normal((T, K)) * 2).astype(np.float16)
+        up = rng.standard_normal((T, K)).astype(np.float16)
+        Y = ops.w8a8_gemm_silu_mul(dev(q), dev(s_), dev(gate), dev(up), g)
+        rq, rs, _ = ref.silu_mul_quant(gate, up, g)
+    else:
+        resid = entry == "rms_resid"
+        h_out = torch.empty((T, K), dtype=torch.float16, device="cuda")
+        Y = ops.w8a8_gemm_rms(dev(q), dev(s_), dev(x), dev(gam), 1e-6, g,
+                              resid=dev(res) if resid else None, h_out=h_out)
+        h = ref.residual_add(x, res) if resid else x
+        rq, rs, _ = ref.rms_norm_quant(h, gam, 1e-6, g)
+        assert same(host(h_out), h)
+    assert same(host(Y), ref.gemm_quantized(q, s_, g, rq, rs))
 
 
 # ------------------------------------------------------- decode stack ----
