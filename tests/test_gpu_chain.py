@@ -143,6 +143,57 @@ def test_chain_step_kinds_bitexact(g, ks):
     ch.close()
 
 
+@pytest.mark.parametrize("case", range(4))
+def test_chain_random_steps(case):
+    """Seeded random step lists (row counts, K, prologue and epilogue kinds,
+    K % g often nonzero), every step against the oracle."""
+    rng = np.random.default_rng(900 + case)
+    g = int(rng.choice([64, 128, 256]))
+    steps, checks, keep = [], [], []
+    for i in range(int(rng.integers(3, 7))):
+        pro = int(rng.choice([0, 2]))
+        epi = int(rng.choice([0, 0, 1]))
+        K = int(rng.integers(max(1, g // 16), (4096 if pro else 8192) // 16 + 1)) * 16
+        M = int(rng.integers(2, 1200)) * (2 if epi else 1)
+        q, s_ = ref.quantize_weights(synth.weights_f16(M, K, seed=case * 10 + i), g)
+        x = synth.activations_f16(1, K, seed=case * 10 + i + 100)
+        st = dict(w=dev(q), w_scale=dev(s_), x=dev(x))
+        if pro == 2:
+            x2 = synth.activations_f16(1, K, seed=case * 10 + i + 200)
+            gm = synth.gamma_f16(K, seed=case * 10 + i)
+            h_out = torch.empty(K, dtype=torch.float16, device="cuda")
+            st.update(x2=dev(x2), gamma=dev(gm), h_out=h_out, prologue=2, eps=1e-6)
+            h = ref.residual_add(x, x2)
+            xq, xs, _ = ref.rms_norm_quant(h, gm, 1e-6, g)
+        else:
+            h = None
+            xq, xs = ref.quantize_activations(x, g)
+        y = ref.gemm_quantized(q, s_, g, xq, xs)
+        if epi:
+            st["epilogue"] = 1
+            _, _, y = ref.silu_mul_quant(np.ascontiguousarray(y[:, 0::2]),
+                                         np.ascontiguousarray(y[:, 1::2]), g)
+        out = torch.empty(y.shape[1], dtype=torch.float16, device="cuda")
+        st["y"] = out
+        steps.append(st)
+        checks.append((out, y[0], st.get("h_out"), None if h is None else h[0]))
+    ch = ops.Chain(steps, g)
+    try:
+        for rep in range(2):
+            for out, _, ho, _ in checks:
+                out.fill_(0)
+                if ho is not None:
+                    ho.fill_(0)
+            ch.run()
+            assert ch.status() == 0
+            for i, (out, want, ho, hw) in enumerate(checks):
+                assert same(host(out), want), (case, rep, i)
+                if ho is not None:
+                    assert same(host(ho), hw), (case, rep, i, "h_out")
+    finally:
+        ch.close()
+
+
 def test_chain_gives_up_and_recovers():
     """With no polls allowed, a step that has to wait for its predecessor
     gives up: every workgroup leaves, the status reports it, and the next run
