@@ -236,3 +236,29 @@ def test_prefill_attention_unaligned_buffers():
     got = host(do)[1:].reshape(n_q, T, D).astype(np.float64)
     want, aw = ref.prefill_attention(q, k, v, sc)
     assert np.all(np.abs(got - want) <= ref.attention_tolerance(want, aw))
+
+
+def _attn_sweep(n=10, seed=31):
+    """Seeded random attention shapes: token counts, GQA ratios, head dims
+    of the fused kernel and of the any-shape one, windows, input scales."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        n_kv = int(rng.choice([1, 2, 4]))
+        n_q = n_kv * int(rng.choice([1, 2, 3, 4, 8]))
+        D = int(rng.choice([32, 64, 128, 40, 96, 24, 160]))
+        T = int(rng.integers(1, 400))
+        window = int(rng.choice([0, 0, int(rng.integers(1, 300))]))
+        scale = float(rng.choice([0.5, 1.0, 2.0]))
+        out.append((T, n_q, n_kv, D, window, scale))
+    return out
+
+
+@pytest.mark.parametrize("T,n_q,n_kv,D,window,scale", _attn_sweep())
+def test_prefill_attention_random_shapes(T, n_q, n_kv, D, window, scale):
+    what = "attn sweep T=%d n_q=%d n_kv=%d D=%d window=%d scale=%g" % (T, n_q, n_kv, D, window,
+                                                                       scale)
+    print(what, flush=True)
+    rng = np.random.default_rng(T * 13 + D)
+    q, k, v = ref.qkv_split_gqa(qkv_rand(rng, T, n_q, n_kv, D, scale), n_q, n_kv, D)
+    check_attention(q, k, v, 1.0 / np.sqrt(D), window, what)
