@@ -75,3 +75,27 @@ def test_noalloc_rejects_oversized_shape():
     assert "maximum" in str(e.value)
     # the library still works afterwards
     run_pair(4, 64, 512, 64, seed=6)
+
+
+def _noalloc_sweep(n=10, seed=55):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        N = int(rng.choice([1, int(rng.integers(2, 17)), int(rng.integers(17, 700))]))
+        M = int(rng.integers(1, 3000 if N <= 16 else 1000))
+        K = int(rng.integers(1, 300 if N <= 16 else 120)) * 16
+        g = int(rng.choice([64, 128, 256, 512]))
+        if N * M * K > 1.2e9:
+            continue
+        if _lib.lib().fa_noalloc_scratch_bytes(M, N, K, g) > _lib.FA_NOALLOC_SCRATCH_BYTES:
+            continue
+        out.append((N, M, K, g))
+    return out
+
+
+@pytest.mark.parametrize("N,M,K,g", _noalloc_sweep())
+def test_noalloc_random_shapes(N, M, K, g):
+    """Seeded random shapes, each against fa_w8a8_gemm (or, where that
+    splits K, the oracle), one call after another on the shared array."""
+    print("noalloc sweep N=%d M=%d K=%d g=%d" % (N, M, K, g), flush=True)
+    run_pair(N, M, K, g, seed=N + M + K)
