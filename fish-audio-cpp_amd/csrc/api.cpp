@@ -619,6 +619,78 @@ static int gemm_swiglu_impl(const int8_t* W13, const uint16_t* w13_scale, int gr
     return FA_OK;
 }
 
+static int gemm_swiglu_sep_impl(const int8_t* W1, const uint16_t* w1_scale, const int8_t* W3,
+                                const uint16_t* w3_scale, int group_size,
+                                const uint16_t* act_scale1, const uint16_t* smooth_inv1,
+                                const uint16_t* act_scale3, const uint16_t* smooth_inv3,
+                                const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                                const uint16_t* gamma, float eps, uint16_t* act, int F, int N,
+                                int K, void* stream) {
+    const char* fn = "fa_w8a8_gemm_swiglu_sep";
+    g_err.clear();
+    int rc = check_dims(fn, F, N, K);
+    if (rc) return rc;
+    if (F == 0 || N == 0) return FA_OK;
+    if (F > (1 << 29)) return fail(FA_ERR_INVALID_ARG, "%s: F=%d too large", fn, F);
+    if (!W1 || !w1_scale || !W3 || !w3_scale || !x || !act)
+        return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
+    if (!gamma && (resid || h_out))
+        return fail(FA_ERR_INVALID_ARG, "%s: resid / h_out need the RMSNorm (gamma)", fn);
+    if (resid && !h_out)
+        return fail(FA_ERR_INVALID_ARG, "%s: a residual addend needs h_out", fn);
+    const size_t nk = (size_t)N * (size_t)K;
+    if (h_out && (overlaps(h_out, nk, x, nk) || overlaps(h_out, nk, resid, nk)))
+        return fail(FA_ERR_INVALID_ARG, "%s: h_out overlaps x or resid", fn);
+    const size_t nf = (size_t)N * (size_t)F;
+    if (overlaps(act, nf, x, nk) || overlaps(act, nf, resid, nk) || overlaps(act, nf, h_out, nk) ||
+        overlaps(act, nf, gamma, (size_t)K))
+        return fail(FA_ERR_INVALID_ARG, "%s: act overlaps an input or h_out", fn);
+    if (gamma && K > 65536) return fail(FA_ERR_INVALID_ARG, "%s: K=%d exceeds 65536", fn, K);
+    hipStream_t s = (hipStream_t)stream;
+    const int M = 2 * F;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    if (N == 1 && aligned16(W1) && aligned16(W3) && aligned16(x) && (!gamma || aligned16(gamma)) &&
+        (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, gamma ? 2 : 0, 2);
+        if (gp.kind == 2) {
+            FA_HIP(fa::launch_gemv(gp, W1, w1_scale, nullptr, nullptr, x, act_scale1, smooth_inv1,
+                                   act, nullptr, 0, 0, 0, 0, M, N, K, g, G, s, resid, gamma, eps,
+                                   resid ? h_out : nullptr, W3, w3_scale, act_scale3,
+                                   smooth_inv3));
+            if (!resid && h_out)
+                FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
+            return FA_OK;
+        }
+    }
+    // separate launches: gate into act, up into scratch, then silu and mul
+    Workspace* ws = nullptr;
+    rc = current_ws(&ws);
+    if (rc) return rc;
+    void* p = ws->yt;
+    rc = grow(&p, &ws->yt_bytes, nf * 2, s);
+    ws->yt = (uint16_t*)p;
+    if (rc) return rc;
+    uint16_t* up = ws->yt;
+    if (gamma) {
+        rc = fa_w8a8_gemm_rms(W1, w1_scale, group_size, act_scale1, smooth_inv1, x, resid, h_out,
+                              gamma, eps, act, F, N, K, stream);
+        if (rc) return rc;
+        rc = fa_w8a8_gemm_rms(W3, w3_scale, group_size, act_scale3, smooth_inv3,
+                              resid ? h_out : x, nullptr, nullptr, gamma, eps, up, F, N, K, stream);
+    } else {
+        rc = fa_w8a8_gemm(W1, w1_scale, group_size, act_scale1, smooth_inv1, x, act, F, N, K,
+                          stream);
+        if (rc) return rc;
+        rc = fa_w8a8_gemm(W3, w3_scale, group_size, act_scale3, smooth_inv3, x, up, F, N, K,
+                          stream);
+    }
+    if (rc) return rc;
+    FA_HIP(fa::launch_elementwise(0, act, nullptr, (int64_t)nf, s));   // silu_forward
+    FA_HIP(fa::launch_elementwise(1, act, up, (int64_t)nf, s));        // mul_forward
+    return FA_OK;
+}
+
 static int gemm_silu_mul_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
                           const uint16_t* act_scale, const uint16_t* smooth_inv,
                           const uint16_t* gate, const uint16_t* up, uint16_t* Y, int M, int N,
@@ -693,6 +765,23 @@ int fa_w8a8_gemm_silu_mul(const int8_t* W, const uint16_t* w_scale, int group_si
                                       M, N, K, stream);
     if (rc == FA_OK && M > 0 && N > 0)
         pc.finish("fa_w8a8_gemm_silu_mul", M, N, K, group_size, act_scale, smooth_inv);
+    return rc;
+}
+
+int fa_w8a8_gemm_swiglu_sep(const int8_t* W1, const uint16_t* w1_scale, const int8_t* W3,
+                            const uint16_t* w3_scale, int group_size,
+                            const uint16_t* act_scale1, const uint16_t* smooth_inv1,
+                            const uint16_t* act_scale3, const uint16_t* smooth_inv3,
+                            const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                            const uint16_t* gamma, float eps, uint16_t* act, int F, int N, int K,
+                            void* stream) {
+    ProfCall pc(stream);
+    const int rc = gemm_swiglu_sep_impl(W1, w1_scale, W3, w3_scale, group_size, act_scale1,
+                                        smooth_inv1, act_scale3, smooth_inv3, x, resid, h_out,
+                                        gamma, eps, act, F, N, K, stream);
+    if (rc == FA_OK && F > 0 && N > 0)
+        pc.finish("fa_w8a8_gemm_swiglu_sep", 2 * F, N, K, group_size,
+                  act_scale1 || act_scale3, smooth_inv1 || smooth_inv3);
     return rc;
 }
 

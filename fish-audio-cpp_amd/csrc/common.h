@@ -140,7 +140,8 @@ struct GemvPlan {
     bool lc = false; // mfma: all terms in LDS, one chain lane per output
     int pro = 0;     // dot with in-kernel quantization: fused prologue (0 plain,
                      // 1 SiLU*mul, 2 residual + RMSNorm)
-    int epi = 0;     // dot: 1 = SwiGLU pair epilogue (rows interleaved w1 / w3)
+    int epi = 0;     // dot: 1 = SwiGLU pair epilogue (rows interleaved w1 / w3),
+                     // 2 = the same on separate w1 / w3 quantized apart
     int grid = 0, block = 0;
     size_t lds = 0;
 };
@@ -166,7 +167,10 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
                        int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
                        int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream,
                        const uint16_t* x2 = nullptr, const uint16_t* gamma = nullptr,
-                       float eps = 0.0f, uint16_t* h_out = nullptr);
+                       float eps = 0.0f, uint16_t* h_out = nullptr,
+                       const int8_t* w3 = nullptr, const uint16_t* w3_scale = nullptr,
+                       const uint16_t* act_scale3 = nullptr,
+                       const uint16_t* smooth_inv3 = nullptr);
 
 // Prefill GEMM on int8 MFMA with LDS-staged tiles.
 hipError_t launch_gemm(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,

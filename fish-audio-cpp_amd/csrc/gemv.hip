@@ -94,6 +94,9 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi)
         const int Kp = (K + 15) & ~15;
         p.lds = (size_t)Kp + (size_t)((G + 3) & ~3) * sizeof(float);   // xs padded for float4 reads
         if (pro == 2) p.lds += (size_t)Kp * 2 + 33 * sizeof(float);      // fp16 row, warp sums
+        if (epi == 2)   // the fp16 row area, then the up weight's codes and scales
+            p.lds = (((size_t)Kp + (size_t)((G + 3) & ~3) * 4 + (size_t)Kp * 2 + 33 * 4 + 15) &
+                     ~(size_t)15) + (size_t)Kp + (size_t)((G + 3) & ~3) * 4;
         p.pro = pro;
         if (g < 16) return GemvPlan{};
         if (p.lds > 64 * 1024) return GemvPlan{};
@@ -134,16 +137,19 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
                        const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
                        int32_t* dbg_partials, int dbg_row0, int dbg_rows, int dbg_tok0,
                        int dbg_toks, int M, int N, int K, int g, int G, hipStream_t stream,
-                       const uint16_t* x2, const uint16_t* gamma, float eps, uint16_t* h_out) {
+                       const uint16_t* x2, const uint16_t* gamma, float eps, uint16_t* h_out,
+                       const int8_t* w3, const uint16_t* w3_scale, const uint16_t* act_scale3,
+                       const uint16_t* smooth_inv3) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
-    const ProArgs pro{x2, gamma, h_out, eps};
+    const ProArgs pro{x2, gamma, h_out, eps, w3, w3_scale, act_scale3, smooth_inv3};
     if (p.kind == 1 || p.kind == 2) {
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)
         if (qx != (p.block == kDotWavesQx * 64)) return hipErrorInvalidValue;   // planned for the other input
         if (p.pro == 2 && !gamma) return hipErrorInvalidValue;
         if (p.epi && (p.kind != 2 || !qx || (M & 1))) return hipErrorInvalidValue;
-        DotFn fn = p.epi ? dot_swiglu(p.pro, K, p.kd, lgl)
+        if (p.epi == 2 && (!w3 || !w3_scale)) return hipErrorInvalidValue;
+        DotFn fn = p.epi ? dot_swiglu(p.pro, K, p.kd, lgl, p.epi == 2)
                  : p.pro ? dot_pro(p.kind, p.pro, K, p.kd, lgl)
                          : dot_plain(p.kind, qx, K, p.kd, lgl);
         // One workgroup per row block on staged codes.  With in-kernel

@@ -6,7 +6,10 @@
 namespace fa {
 namespace gv {
 
-DotFn dot_swiglu(int pro, int K, int kd, int lgl) {
+DotFn dot_swiglu(int pro, int K, int kd, int lgl, bool sep) {
+    if (sep)   // separate w1 / w3, each with its own quantization companions
+        return pro == 2 ? dot_for_xv<2, true, kDotWavesQx, 2, 2>(K, kd, lgl)
+                        : dot_for_xv<2, true, kDotWavesQx, 0, 2>(K, kd, lgl);
     return pro == 2 ? dot_for_xv<2, true, kDotWavesQx, 2, 1>(K, kd, lgl)
                     : dot_for_xv<2, true, kDotWavesQx, 0, 1>(K, kd, lgl);
 }

@@ -65,6 +65,12 @@ struct ProArgs {
     const uint16_t* gamma;
     uint16_t* h_out;
     float eps;
+    // EPI 2: the up weight (w3), its scales and its own quantization
+    // companions (the gate weight w1 comes as W / w_scale)
+    const int8_t* w3;
+    const uint16_t* w3_scale;
+    const uint16_t* act_scale3;
+    const uint16_t* smooth_inv3;
 };
 
 // ------------------------------------------------------------ N == 1 ----
@@ -152,14 +158,18 @@ __device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __re
                                          const uint16_t* __restrict__ act_scale,
                                          const uint16_t* __restrict__ smooth_inv, int K, int lg_g,
                                          int G, const ProArgs& pro, int tid, bool write_h,
-                                         int8_t* xq_s, float* xs_s, uint16_t* h_s, float* red_s) {
+                                         int8_t* xq_s, float* xs_s, uint16_t* h_s, float* red_s,
+                                         int8_t* xq2_s = nullptr, float* xs2_s = nullptr,
+                                         const uint16_t* __restrict__ act_scale2 = nullptr,
+                                         const uint16_t* __restrict__ smooth_inv2 = nullptr) {
     // Chunk c holds x[8c, 8c + 8); chunk c of thread tid is tid + i * NT,
     // so a K-group (g / 8 chunks) lies in g / 8 consecutive lanes of one
     // wave.  Its |v| maximum (exact in any order) comes from xor shuffles,
     // then scale and int8 codes are formed in registers: no atomics and a
     // single barrier (the caller's) before the codes are read.
     const int glanes = 1 << (lg_g - 3);
-    auto chunk = [&](int c, const v4i& raw) {
+    auto chunk = [&](int c, const v4i& raw, const uint16_t* __restrict__ act_scale,
+                     const uint16_t* __restrict__ smooth_inv, int8_t* xq_s, float* xs_s) {
         const int k = c * 8;
         const bool ok = k < K;
         const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
@@ -261,11 +271,18 @@ __device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __re
         }
     }
 #pragma unroll
-    for (int i = 0; i < XV; ++i) chunk(tid + i * NT, in.xr[i]);
+    for (int i = 0; i < XV; ++i) chunk(tid + i * NT, in.xr[i], act_scale, smooth_inv, xq_s, xs_s);
+    if (xq2_s) {   // a second weight's own companions (wave-uniform)
+#pragma unroll
+        for (int i = 0; i < XV; ++i)
+            chunk(tid + i * NT, in.xr[i], act_scale2, smooth_inv2, xq2_s, xs2_s);
+    }
     if constexpr (PRO == 0) {
         for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
             const int c = c0 + tid;
-            chunk(c, *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8)));
+            const v4i raw = *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8));
+            chunk(c, raw, act_scale, smooth_inv, xq_s, xs_s);
+            if (xq2_s) chunk(c, raw, act_scale2, smooth_inv2, xq2_s, xs2_s);
         }
     }
 }
@@ -313,6 +330,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     int nblocks, ProArgs pro) {
     static_assert(PRO == 0 || QX, "prologues need in-kernel quantization");
     static_assert(EPI == 0 || R == 2, "the SwiGLU pair needs two rows per wave");
+    static_assert(EPI != 2 || QX, "separate w1 / w3 quantize in-kernel");
     constexpr int RL = 64 / R;            // lanes per row
     constexpr int PB = RL * 16;           // bytes of a row per pass
     constexpr int GPP = RL / LG;          // groups per row per pass
@@ -325,6 +343,10 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     // PRO 2: the fp16 row [Kp] and 32 warp sums + the scale after xs_s
     uint16_t* h_s = reinterpret_cast<uint16_t*>(xs_s + ((G + 3) & ~3));
     float* red_s = reinterpret_cast<float*>(h_s + Kp);
+    // EPI 2: the up weight's codes [Kp] and scales [G] after the PRO 2 area
+    int8_t* xq3_s = reinterpret_cast<int8_t*>(lds) + (((size_t)Kp + 4 * ((G + 3) & ~3) + 2 * Kp +
+                                                        33 * 4 + 15) & ~(size_t)15);
+    float* xs3_s = reinterpret_cast<float*>(xq3_s + Kp);
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -362,18 +384,27 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         const bool live = l_blk < nblocks;
         const int row = row_of_blk(live ? l_blk : blockIdx.x);
         const int rowc = row < M ? row : M - 1;
-        const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
         const int k = l_pass * PB + lane_k;
         const bool ok = live && k < K;
         const int kk = ok ? k : 0;
         // no select on the loaded value (that would wait for the load here):
         // bytes past K meet zero activations in consume()
-        const v4i wa = ld16(wrow + kk);
-        if constexpr ((kAb & 2) == 0)
-            sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
-        else
-            sc[slot] = (uint16_t)kk;
-        a[slot] = wa;
+        if constexpr (EPI == 2) {
+            // row 2i: gate weight row i, row 2i + 1: up weight row i
+            const int8_t* wb = (rowc & 1) ? pro.w3 : W;
+            const uint16_t* sb = (rowc & 1) ? pro.w3_scale : w_scale;
+            const int pr = rowc >> 1;
+            a[slot] = ld16(wb + (size_t)pr * K + kk);
+            sc[slot] = sb[G == 1 ? (size_t)pr : (size_t)pr * G + (kk >> lg_g)];
+        } else {
+            const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
+            const v4i wa = ld16(wrow + kk);
+            if constexpr ((kAb & 2) == 0)
+                sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
+            else
+                sc[slot] = (uint16_t)kk;
+            a[slot] = wa;
+        }
         if (++l_pass == passes) {
             l_pass = 0;
             l_blk += gridDim.x;
@@ -395,8 +426,13 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
             *reinterpret_cast<v4i*>(xq_s + k) = ld16(x_q + k);
         for (int i = tid + NT; i < G; i += NT) xs_s[i] = x_scale[i];
     } else {
-        qx_stage<XV, NT, PRO>(qin, X, act_scale, smooth_inv, K, lg_g, G, pro, tid,
-                              blockIdx.x == 0, xq_s, xs_s, h_s, red_s);
+        if constexpr (EPI == 2)
+            qx_stage<XV, NT, PRO>(qin, X, act_scale, smooth_inv, K, lg_g, G, pro, tid,
+                                  blockIdx.x == 0, xq_s, xs_s, h_s, red_s, xq3_s, xs3_s,
+                                  pro.act_scale3, pro.smooth_inv3);
+        else
+            qx_stage<XV, NT, PRO>(qin, X, act_scale, smooth_inv, K, lg_g, G, pro, tid,
+                                  blockIdx.x == 0, xq_s, xs_s, h_s, red_s);
     }
     if constexpr ((kAb & 1) == 0) __syncthreads();
 
@@ -408,7 +444,8 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     auto consume = [&](int slot) {
         const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
         const int k = kbase + lane_k;
-        v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xq_s + (k < K ? k : 0));
+        const int8_t* xqr = (EPI == 2 && rsub == 1) ? xq3_s : xq_s;   // EPI 2: the row's codes
+        v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xqr + (k < K ? k : 0));
         if (k >= K) b = zero;
         int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
         p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
@@ -426,17 +463,22 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         } else {
             // group order within the pass: slot j of every row; the pass's
             // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
-            float xsv[GPP];
-            const float* xp = xs_s + (kbase >> lg_g);
-            if constexpr (GPP == 4) {
-                const float4 v = *reinterpret_cast<const float4*>(xp);
-                xsv[0] = v.x; xsv[1] = v.y; xsv[2] = v.z; xsv[3] = v.w;
-            } else if constexpr (GPP == 2) {
-                const float2 v = *reinterpret_cast<const float2*>(xp);
-                xsv[0] = v.x; xsv[1] = v.y;
-            } else {
+            // (EPI 2: row slot 1 takes the up weight's token scales)
+            constexpr int NXS = EPI == 2 ? 2 : 1;
+            float xsv[NXS][GPP];
 #pragma unroll
-                for (int j = 0; j < GPP; ++j) xsv[j] = xp[j];
+            for (int q = 0; q < NXS; ++q) {
+                const float* xp = (q ? xs3_s : xs_s) + (kbase >> lg_g);
+                if constexpr (GPP == 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(xp);
+                    xsv[q][0] = v.x; xsv[q][1] = v.y; xsv[q][2] = v.z; xsv[q][3] = v.w;
+                } else if constexpr (GPP == 2) {
+                    const float2 v = *reinterpret_cast<const float2*>(xp);
+                    xsv[q][0] = v.x; xsv[q][1] = v.y;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < GPP; ++j) xsv[q][j] = xp[j];
+                }
             }
 #pragma unroll
             for (int j = 0; j < GPP; ++j) {
@@ -447,14 +489,14 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
                         const float tj = __builtin_bit_cast(
                             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
                                                              r * RL + j * LG));
-                        acc[r] = __builtin_fmaf(tj, xsv[j], acc[r]);
+                        acc[r] = __builtin_fmaf(tj, xsv[NXS == 2 ? r : 0][j], acc[r]);
                     }
                 }
             }
         }
         if (++c_pass == passes) {
             const int row = row_of_blk(c_blk);
-            if constexpr (EPI == 1) {
+            if constexpr (EPI != 0) {
                 // every lane holds both chains; lane 0 (row slot 0: the even
                 // gate row) stores the pair's activation
                 if (lane == 0 && row + 1 < M) {
@@ -682,7 +724,7 @@ using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const floa
 // (kd: ring depth 3..5; lgl: log2 of the lanes per group, 2..5).
 DotFn dot_plain(int R, bool qx, int K, int kd, int lgl);        // gemv_dot.hip
 DotFn dot_pro(int R, int pro, int K, int kd, int lgl);          // gemv_dot_pro.hip
-DotFn dot_swiglu(int pro, int K, int kd, int lgl);              // gemv_dot_swiglu.hip
+DotFn dot_swiglu(int pro, int K, int kd, int lgl, bool sep = false);  // gemv_dot_swiglu.hip
 
 // Instantiation helpers for those units.
 template <int R, int KD, bool QX, int XV, int NWV, int PRO, int EPI>

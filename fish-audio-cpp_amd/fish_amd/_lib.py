@@ -78,6 +78,8 @@ SIGNATURES = {
     "fa_w8a8_gemm_rms": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _f, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_silu_mul": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "fa_gemm_fp16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "fa_w8a8_gemm_swiglu_sep": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _f, _p,
+                                     _i, _i, _i, _p]),
     "fa_profile_enable": (_i, [_i]),
     "fa_profile_summary": (ctypes.c_size_t, [_p, ctypes.c_size_t]),
     "fa_profile_reset": (None, []),

@@ -101,6 +101,57 @@ class DecodeStack:
         ops.w8a8_gemm(L.W, L.scale, x, L.g, out=out)
 
     def run_stack_awq(self):
+        """The calibrated (AWQ) layout, four launches per layer:
+
+            qkv      fa_w8a8_gemm_rms         h' = h + down_prev; attention_norm(h') * smooth_qkv
+            o        fa_w8a8_gemm             the q slice of qkv's output
+            gate_up  fa_w8a8_gemm_swiglu_sep  h'' = h' + o; ffn_norm(h''), quantized once with
+                                              smooth_w1 for w1 and once with smooth_w3 for w3;
+                                              silu(gate) * up
+            down     fa_w8a8_gemm             act
+
+        The same values as run_stack_awq_unfused, which follows the reference's
+        separate calls (dual_ar_engine.cc:576-648 with each weight's QuantMeta,
+        :253-275)."""
+        assert self.awq
+        g, T = self.g, self.T
+        l_ = ops.lib()
+        s = ops._stream()
+        cur, nxt = self.h, self.h_alt
+        if T == 1:
+            o_in = self.y["qkv"]
+        for li, lay in enumerate(self.layers):
+            L = lay["qkv"]
+            resid = None if li == 0 else self.y["down"].data_ptr()
+            ops.check(l_.fa_w8a8_gemm_rms(L.W.data_ptr(), L.scale.data_ptr(), g, None,
+                                          lay["qkv_smooth"].data_ptr(), cur.data_ptr(), resid,
+                                          None if li == 0 else nxt.data_ptr(),
+                                          lay["attn_norm"].data_ptr(), 1e-6,
+                                          self.y["qkv"].data_ptr(), L.N, T, L.K, s))
+            if li != 0:
+                cur, nxt = nxt, cur
+            if T != 1:
+                self.o_in.copy_(self.y["qkv"][:, :Q_DIM])
+                o_in = self.o_in
+            L = lay["o"]
+            ops.check(l_.fa_w8a8_gemm(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                      o_in.data_ptr(), self.y["o"].data_ptr(), L.N, T, L.K, s))
+            L1, L3 = lay["w1"], lay["w3"]
+            ops.check(l_.fa_w8a8_gemm_swiglu_sep(
+                L1.W.data_ptr(), L1.scale.data_ptr(), L3.W.data_ptr(), L3.scale.data_ptr(), g,
+                None, lay["w1_smooth"].data_ptr(), None, lay["w3_smooth"].data_ptr(),
+                cur.data_ptr(), self.y["o"].data_ptr(), nxt.data_ptr(),
+                lay["ffn_norm"].data_ptr(), 1e-6, self.act.data_ptr(), L1.N, T, L1.K, s))
+            cur, nxt = nxt, cur
+            L = lay["down"]
+            ops.check(l_.fa_w8a8_gemm(L.W.data_ptr(), L.scale.data_ptr(), g, None, None,
+                                      self.act.data_ptr(), self.y["down"].data_ptr(), L.N, T,
+                                      L.K, s))
+        ops.check(l_.fa_residual_add(cur.data_ptr(), self.y["down"].data_ptr(), T * HIDDEN, s))
+        if cur is not self.h:
+            self.h.copy_(cur)
+
+    def run_stack_awq_unfused(self):
         """The calibrated (AWQ) layout, five launches per layer:
 
             qkv   fa_w8a8_gemm_rms       h' = h + down_prev; attention_norm(h') * smooth_qkv
@@ -154,9 +205,11 @@ class DecodeStack:
             self.h.copy_(cur)
 
     def awq_stack_bytes(self):
-        """Algorithmic bytes of one run_stack_awq pass: int8 W + fp16 scales,
-        the three smooth_inv vectors, gamma twice, and each linear's fp16
-        activations in and out (silu_mul reads gate and up)."""
+        """Algorithmic bytes of one calibrated-layout pass, counted as the
+        reference moves them (both run_stack_awq variants use this count):
+        int8 W + fp16 scales, the three smooth_inv vectors, gamma twice, and
+        each of the five linears' fp16 activations in and out (silu_mul
+        reads gate and up)."""
         tot = 0
         for lay in self.layers:
             for name in ("qkv", "o", "w1", "w3", "down"):

@@ -109,6 +109,29 @@ def w8a8_gemm_swiglu(W13, w13_scale, x, group_size, gamma=None, eps=1e-6, resid=
     return Y
 
 
+def w8a8_gemm_swiglu_sep(W1, w1_scale, W3, w3_scale, x, group_size, gamma=None, eps=1e-6,
+                         resid=None, h_out=None, act_scale1=None, smooth_inv1=None,
+                         act_scale3=None, smooth_inv3=None, out=None):
+    """act [N, F] = fp16(silu(x @ w1.T)) * (x @ w3.T) on separate w1 / w3, each
+    input quantized with its weight's own companions."""
+    for t, n in ((W1, "W1"), (W3, "W3")):
+        _need(t, torch.int8, n)
+    for t, n in ((w1_scale, "w1_scale"), (w3_scale, "w3_scale"), (x, "x"), (gamma, "gamma"),
+                 (resid, "resid"), (h_out, "h_out")):
+        _need(t, torch.float16, n)
+    F, K = W1.shape
+    if tuple(W3.shape) != (F, K):
+        raise ValueError("W1 %s and W3 %s differ" % (tuple(W1.shape), tuple(W3.shape)))
+    N = x.shape[0]
+    Y = out if out is not None else torch.empty((N, F), dtype=torch.float16, device=x.device)
+    check(lib().fa_w8a8_gemm_swiglu_sep(_ptr(W1), _ptr(w1_scale), _ptr(W3), _ptr(w3_scale),
+                                        group_size, _ptr(act_scale1), _ptr(smooth_inv1),
+                                        _ptr(act_scale3), _ptr(smooth_inv3), _ptr(x), _ptr(resid),
+                                        _ptr(h_out), _ptr(gamma), eps, _ptr(Y), F, N, K,
+                                        _stream()))
+    return Y
+
+
 def interleave_rows(a, b):
     """Rows of a and b interleaved: row 2i = a[i], row 2i + 1 = b[i]."""
     return torch.stack((a, b), dim=1).reshape(2 * a.shape[0], *a.shape[1:]).contiguous()

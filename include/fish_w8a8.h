@@ -117,6 +117,28 @@ int fa_w8a8_gemm_swiglu(const int8_t* W13, const uint16_t* w13_scale, int group_
                         const uint16_t* gamma, float eps, uint16_t* act, int F, int N, int K,
                         void* stream);
 
+/* SwiGLU over separate w1 / w3 weights, each with its own quantization
+ * companions -- the layout of a calibrated dual_ar.bin, where w1 and w3 carry
+ * different `_smooth_inv` (or `_act_scale`) vectors, so their inputs quantize
+ * differently and the two cannot share one interleaved weight
+ * (tools/step2_export_w8a8.py:477; the engine's two int8_dequant_gemm_fp16
+ * calls, src/engine/dual_ar_engine.cc:640-644, with silu_forward and
+ * mul_forward).  act [N, F] = fp16(fp16(silu(gate)) * up) with
+ * gate = x' @ w1.T quantized with (act_scale1, smooth_inv1) and
+ * up = x' @ w3.T quantized with (act_scale3, smooth_inv3); x' is
+ * rms_norm(x (+ resid), gamma) when gamma is non-NULL (h_out then receives
+ * x + resid, or x), else x.  W1 / W3 are int8 [F, K] with fp16 scales
+ * [F, G] each.  One launch at N == 1 (both quantizations in the GEMV
+ * prologue); separate launches otherwise.  No counterpart entry point in the
+ * reference. */
+int fa_w8a8_gemm_swiglu_sep(const int8_t* W1, const uint16_t* w1_scale, const int8_t* W3,
+                            const uint16_t* w3_scale, int group_size,
+                            const uint16_t* act_scale1, const uint16_t* smooth_inv1,
+                            const uint16_t* act_scale3, const uint16_t* smooth_inv3,
+                            const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                            const uint16_t* gamma, float eps, uint16_t* act, int F, int N, int K,
+                            void* stream);
+
 /* Fused prologue + linear for the FFN down projection: the quantizer sees
  * fp16(fp16(silu(gate)) * up) (silu_forward then mul_forward,
  * ffn_activations.cu:12-17, 35-39), then fa_w8a8_gemm's quantizer and linear.

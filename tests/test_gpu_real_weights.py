@@ -171,16 +171,19 @@ def test_gemm_swiglu_one_token_shared_companions(g, mode, variant):
 
 # ------------------------------------------------- calibrated decode stack ----
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("g,T,layers", [(256, 1, 3), (64, 1, 2), (256, 2, 2)])
-def test_awq_decode_stack_bitexact(g, T, layers):
-    """DecodeStack(awq=True).run_stack_awq: wqkv, w1 and w3 each carry their
-    own smooth_inv (the calibrated dual_ar.bin layout), so w1 and w3 run as
-    separate linears on differently quantized inputs.  The final residual
-    stream equals the oracle's sequence of separate functions bit for bit."""
+def test_awq_decode_stack_bitexact(g, T, layers, fused):
+    """DecodeStack(awq=True): wqkv, w1 and w3 each carry their own
+    smooth_inv (the calibrated dual_ar.bin layout), so w1 and w3 see
+    differently quantized inputs -- one fa_w8a8_gemm_swiglu_sep launch
+    (run_stack_awq) or two RMS-fused linears and silu_mul
+    (run_stack_awq_unfused).  The final residual stream equals the oracle's
+    sequence of separate functions bit for bit."""
     from fish_amd.decode_stack import DecodeStack, Q_DIM
     st = DecodeStack(n_layers=layers, g=g, tokens=T, seed=9, awq=True)
     st.h.copy_(st.h0)
-    st.run_stack_awq()
+    (st.run_stack_awq if fused else st.run_stack_awq_unfused)()
     torch.cuda.synchronize()
     h = host(st.h0)
     for lay in st.layers:
@@ -200,6 +203,51 @@ def test_awq_decode_stack_bitexact(g, T, layers):
         xq, xs, _ = ref.silu_mul_quant(gate, up, g)
         h = ref.residual_add(h, lin("down", xq, xs))
     assert same(host(st.h), h)
+
+
+# ------------------------------------------- separate w1 / w3 SwiGLU ----
+
+@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("mode", ["plain", "rms", "rms_resid"])
+@pytest.mark.parametrize("comp", ["smooth", "static", "mixed"])
+@pytest.mark.parametrize("F,K,g", [(9728, 2560, 256), (1531, 2560, 64), (700, 2576, 128)])
+def test_swiglu_sep(F, K, g, comp, mode, T):
+    """fa_w8a8_gemm_swiglu_sep: act = fp16(silu(gate)) * up with gate and up
+    from separate weights whose inputs quantize with their own companions,
+    bit for bit against the oracle's two linears and silu_mul; h_out is the
+    residual stream.  One launch at T == 1, separate launches otherwise."""
+    print("swiglu_sep F=%d K=%d g=%d %s %s T=%d" % (F, K, g, comp, mode, T), flush=True)
+    q1, s1 = make_linear(F, K, g, seed=61)
+    q3, s3 = make_linear(F, K, g, seed=62)
+    x = synth.activations_f16(T, K, seed=63)
+    gam = synth.gamma_f16(K, seed=64)
+    res = synth.activations_f16(T, K, seed=65)
+    if comp == "smooth":
+        a1, m1, a3, m3 = None, smooth_inv_f16(K, 66), None, smooth_inv_f16(K, 67)
+    elif comp == "static":
+        a1, m1, a3, m3 = act_scale_f16(K, g, 68), None, act_scale_f16(K, g, 69, amax=20.0), None
+    else:
+        a1, m1, a3, m3 = None, smooth_inv_f16(K, 70), act_scale_f16(K, g, 71), None
+    h_out = torch.empty((T, K), dtype=torch.float16, device="cuda") if mode != "plain" else None
+    d = dict(W1=dev(q1), s1=dev(s1), W3=dev(q3), s3=dev(s3), x=dev(x), gam=dev(gam), res=dev(res))
+    act = ops.w8a8_gemm_swiglu_sep(
+        d["W1"], d["s1"], d["W3"], d["s3"], d["x"], g,
+        gamma=None if mode == "plain" else d["gam"], eps=1e-6,
+        resid=d["res"] if mode == "rms_resid" else None, h_out=h_out,
+        act_scale1=opt(a1), smooth_inv1=opt(m1), act_scale3=opt(a3), smooth_inv3=opt(m3))
+    h = ref.residual_add(x, res) if mode == "rms_resid" else x
+    def quant(a, m):
+        if mode == "plain":
+            return ref.quantize_activations(h, g, act_scale=a, smooth_inv=m)
+        xq, xs, _ = ref.rms_norm_quant(h, gam, 1e-6, g, act_scale=a, smooth_inv=m)
+        return xq, xs
+    gate = ref.gemm_quantized(q1, s1, g, *quant(a1, m1))
+    up = ref.gemm_quantized(q3, s3, g, *quant(a3, m3))
+    _, _, want = ref.silu_mul_quant(gate, up, g)
+    assert same(host(act), want)
+    if h_out is not None:
+        assert same(host(h_out), h)
+    assert same(host(d["x"]), x)
 
 
 # ------------------------------------------------------- fast decoder ----
