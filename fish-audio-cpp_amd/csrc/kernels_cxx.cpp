@@ -89,6 +89,18 @@ void int8_silu_mul_gemm_fp16(const int8_t* W, const __half* scale, int group_siz
                                 u16(gate), u16(up), u16(Y), M, N, K, stream));
 }
 
+void int8_swiglu_sep_gemm_fp16(const int8_t* W1, const __half* scale1, const int8_t* W3,
+                               const __half* scale3, int group_size, const __half* act_scale1,
+                               const __half* smooth_inv1, const __half* act_scale3,
+                               const __half* smooth_inv3, const __half* x, const __half* resid,
+                               __half* h_out, const __half* gamma, float eps, __half* act, int F,
+                               int N, int K, hipStream_t stream) {
+    check(fa_w8a8_gemm_swiglu_sep(W1, u16(scale1), W3, u16(scale3), group_size, u16(act_scale1),
+                                  u16(smooth_inv1), u16(act_scale3), u16(smooth_inv3), u16(x),
+                                  u16(resid), u16(h_out), u16(gamma), eps, u16(act), F, N, K,
+                                  stream));
+}
+
 void prefill_attention_gpu(const __half* q, const __half* k, const __half* v, __half* out,
                            __half* workspace, int n_q, int n_kv, int T, int D, float sm_scale,
                            void* /*blas_handle_unused*/, hipStream_t stream, int window_size) {

@@ -77,5 +77,12 @@ void int8_silu_mul_gemm_fp16(const int8_t* W, const __half* scale, int group_siz
                              const __half* act_scale, const __half* smooth_inv,
                              const __half* gate, const __half* up, __half* Y, int M, int N, int K,
                              hipStream_t stream = 0);
+// SwiGLU over separate w1 / w3 with their own companions (fa_w8a8_gemm_swiglu_sep).
+void int8_swiglu_sep_gemm_fp16(const int8_t* W1, const __half* scale1, const int8_t* W3,
+                               const __half* scale3, int group_size, const __half* act_scale1,
+                               const __half* smooth_inv1, const __half* act_scale3,
+                               const __half* smooth_inv3, const __half* x, const __half* resid,
+                               __half* h_out, const __half* gamma, float eps, __half* act, int F,
+                               int N, int K, hipStream_t stream = 0);
 
 }  // namespace fish::kernels
