@@ -49,6 +49,8 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+// (the one-token kernels read smooth_inv 16 bytes at a time)
+bool aligned16_or_null(const void* p) { return !p || aligned16(p); }
 
 // Per-thread, per-device grow-only scratch (the reference keeps a thread_local
 // workspace, int8_gemm.cu:31-44).
@@ -374,7 +376,7 @@ static int gemm_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W) && aligned16(X)) {
+    if (N == 1 && aligned16_or_null(smooth_inv) && aligned16(W) && aligned16(X)) {
         // decode: the GEMV quantizes the token itself (one launch, no scratch)
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true);
         if (gp.kind == 1 || gp.kind == 2) {
@@ -473,7 +475,7 @@ int fa_w8a8_gemm_noalloc(const int8_t* W, const uint16_t* w_scale, int group_siz
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W) && aligned16(X)) {
+    if (N == 1 && aligned16_or_null(smooth_inv) && aligned16(W) && aligned16(X)) {
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true);
         if (gp.kind == 1 || gp.kind == 2) {
             FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, X, act_scale, smooth_inv, Y,
@@ -526,7 +528,8 @@ static int gemm_rms_impl(const int8_t* W, const uint16_t* w_scale, int group_siz
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W) && aligned16(x) && aligned16(gamma) &&
+    if (N == 1 && aligned16_or_null(smooth_inv) && aligned16(W) && aligned16(x) &&
+        aligned16(gamma) &&
         (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, 2);
         if (gp.kind == 1 || gp.kind == 2) {
@@ -589,7 +592,8 @@ static int gemm_swiglu_impl(const int8_t* W13, const uint16_t* w13_scale, int gr
     const int M = 2 * F;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W13) && aligned16(x) && (!gamma || aligned16(gamma)) &&
+    if (N == 1 && aligned16_or_null(smooth_inv) && aligned16(W13) && aligned16(x) &&
+        (!gamma || aligned16(gamma)) &&
         (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, gamma ? 2 : 0, 1);
         if (gp.kind == 2) {
@@ -650,7 +654,8 @@ static int gemm_swiglu_sep_impl(const int8_t* W1, const uint16_t* w1_scale, cons
     const int M = 2 * F;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W1) && aligned16(W3) && aligned16(x) && (!gamma || aligned16(gamma)) &&
+    if (N == 1 && aligned16_or_null(smooth_inv1) && aligned16_or_null(smooth_inv3) &&
+        aligned16(W1) && aligned16(W3) && aligned16(x) && (!gamma || aligned16(gamma)) &&
         (!resid || aligned16(resid)) && (!h_out || aligned16(h_out))) {
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, gamma ? 2 : 0, 2);
         if (gp.kind == 2) {
@@ -707,7 +712,8 @@ static int gemm_silu_mul_impl(const int8_t* W, const uint16_t* w_scale, int grou
     hipStream_t s = (hipStream_t)stream;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    if (N == 1 && aligned16(W) && aligned16(gate) && aligned16(up)) {
+    if (N == 1 && aligned16_or_null(smooth_inv) && aligned16(W) && aligned16(gate) &&
+        aligned16(up)) {
         fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, 1);
         if (gp.kind == 1 || gp.kind == 2) {
             FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, gate, act_scale, smooth_inv,

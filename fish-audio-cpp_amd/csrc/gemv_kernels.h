@@ -124,17 +124,26 @@ struct QxIn {
     v4i xr[XV];
     v4i x2r[PRO != 0 ? XV : 1];
     v4i gmr[PRO == 2 ? XV : 1];
+    v4i smr[XV], sm2r[XV];   // smooth_inv chunks of the first / second companions
 };
 
-template <int XV, int NT, int PRO>
+template <int XV, int NT, int PRO, bool SM2 = false>
 __device__ __forceinline__ void qx_load(QxIn<XV, PRO>& in, const uint16_t* __restrict__ X, int K,
-                                        const ProArgs& pro, int tid) {
+                                        const ProArgs& pro, int tid,
+                                        const uint16_t* __restrict__ smooth_inv = nullptr,
+                                        const uint16_t* __restrict__ smooth_inv2 = nullptr) {
     // unconditional loads from clamped addresses (a load under a branch
-    // makes the compiler wait for it on the spot)
+    // makes the compiler wait for it on the spot); without a smooth_inv
+    // vector its chunks re-read X and are not used
+    const uint16_t* sm1 = smooth_inv ? smooth_inv : X;
+    const uint16_t* sm2 = smooth_inv2 ? smooth_inv2 : X;
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
         const int k = (tid + i * NT) * 8;
-        in.xr[i] = *reinterpret_cast<const v4i*>(X + (k < K ? k : K - 8));
+        const int kc = k < K ? k : K - 8;
+        in.xr[i] = *reinterpret_cast<const v4i*>(X + kc);
+        in.smr[i] = *reinterpret_cast<const v4i*>(sm1 + kc);
+        if constexpr (SM2) in.sm2r[i] = *reinterpret_cast<const v4i*>(sm2 + kc);
     }
     // prologue operands: up (PRO 1) or the residual addend (PRO 2; X again
     // when there is none) and gamma
@@ -168,16 +177,20 @@ __device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __re
     // then scale and int8 codes are formed in registers: no atomics and a
     // single barrier (the caller's) before the codes are read.
     const int glanes = 1 << (lg_g - 3);
+    // smv: this chunk's smooth_inv values when loaded ahead (qx_load), else
+    // they are read here
     auto chunk = [&](int c, const v4i& raw, const uint16_t* __restrict__ act_scale,
-                     const uint16_t* __restrict__ smooth_inv, int8_t* xq_s, float* xs_s) {
+                     const uint16_t* __restrict__ smooth_inv, int8_t* xq_s, float* xs_s,
+                     const v4i* smv) {
         const int k = c * 8;
         const bool ok = k < K;
         const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+        const uint16_t* sh = reinterpret_cast<const uint16_t*>(smv);
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             v[e] = h2f(h[e]);
-            if (smooth_inv) v[e] *= h2f(smooth_inv[ok ? k + e : e]);
+            if (smooth_inv) v[e] *= h2f(smv ? sh[e] : smooth_inv[ok ? k + e : e]);
         }
         const int gi = ok ? k >> lg_g : G - 1;
         float sc_;
@@ -271,18 +284,19 @@ __device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __re
         }
     }
 #pragma unroll
-    for (int i = 0; i < XV; ++i) chunk(tid + i * NT, in.xr[i], act_scale, smooth_inv, xq_s, xs_s);
+    for (int i = 0; i < XV; ++i)
+        chunk(tid + i * NT, in.xr[i], act_scale, smooth_inv, xq_s, xs_s, &in.smr[i]);
     if (xq2_s) {   // a second weight's own companions (wave-uniform)
 #pragma unroll
         for (int i = 0; i < XV; ++i)
-            chunk(tid + i * NT, in.xr[i], act_scale2, smooth_inv2, xq2_s, xs2_s);
+            chunk(tid + i * NT, in.xr[i], act_scale2, smooth_inv2, xq2_s, xs2_s, &in.sm2r[i]);
     }
     if constexpr (PRO == 0) {
         for (int c0 = XV * NT; c0 * 8 < K; c0 += NT) {   // K beyond XV * NT * 8 (uniform trip count)
             const int c = c0 + tid;
             const v4i raw = *reinterpret_cast<const v4i*>(X + (c * 8 < K ? c * 8 : K - 8));
-            chunk(c, raw, act_scale, smooth_inv, xq_s, xs_s);
-            if (xq2_s) chunk(c, raw, act_scale2, smooth_inv2, xq2_s, xs2_s);
+            chunk(c, raw, act_scale, smooth_inv, xq_s, xs_s, nullptr);
+            if (xq2_s) chunk(c, raw, act_scale2, smooth_inv2, xq2_s, xs2_s, nullptr);
         }
     }
 }
@@ -370,7 +384,8 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         }
         xsr = x_scale[tid < G ? tid : G - 1];
     } else {
-        qx_load<XV, NT, PRO>(qin, X, K, pro, tid);
+        qx_load<XV, NT, PRO, EPI == 2>(qin, X, K, pro, tid, smooth_inv,
+                                       EPI == 2 ? pro.smooth_inv3 : nullptr);
     }
 
     // ---- weight ring
