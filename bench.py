@@ -364,6 +364,24 @@ def run_secondary(torch, ops, st, args):
                                              "GB/s": round(sa.awq_stack_bytes() / t / 1e9, 1)}
     del sa, g_awq, g_awq5
     torch.cuda.empty_cache()
+    # configs[2] as a whole decode step: 8 tokens, g64, the 36-layer stack
+    # with every prologue (RMSNorm + quant, SiLU * mul) as the entry points
+    # run it at more than one token
+    s8 = DecodeStack(n_layers=args.layers, g=64, tokens=8, seed=13)
+    s8.h.copy_(s8.h0)
+    g_8 = s8.capture(lambda: s8.run_stack())
+    for _ in range(2):
+        g_8.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_8.replay()
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    out["cfg2_stack_g64_m8"] = {"step_ms": round(t * 1e3, 4),
+                                "GB/s": round(s8.stack_bytes() / t / 1e9, 1)}
+    del s8, g_8
+    torch.cuda.empty_cache()
     # configs[4] at g64 (4x the scale bytes)
     s64 = DecodeStack(n_layers=args.layers, g=64, tokens=1, seed=9)
     s64.h.copy_(s64.h0)

@@ -553,12 +553,7 @@ static int gemm_rms_impl(const int8_t* W, const uint16_t* w_scale, int group_siz
     rc = grow(&p, &ws->xs_bytes, (size_t)N * (size_t)G * sizeof(float), s);
     ws->xs = (float*)p;
     if (rc) return rc;
-    uint16_t* h = const_cast<uint16_t*>(x);   // written only when resid is set
-    if (h_out) {
-        FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
-        h = h_out;
-    }
-    FA_HIP(fa::launch_rms_norm_quant(h, resid, gamma, eps, smooth_inv, act_scale, g, G, ws->xq,
+    FA_HIP(fa::launch_rms_norm_quant(x, resid, h_out, gamma, eps, smooth_inv, act_scale, g, G, ws->xq,
                                      ws->xs, nullptr, N, K, s));
     return linear_quantized(fn, W, w_scale, g, G, ws->xq, ws->xs, Y, nullptr, 0, 0, 0, 0, M, N, K,
                             s);
@@ -857,7 +852,7 @@ int fa_rms_norm(const uint16_t* x, const uint16_t* weight, uint16_t* out, int n_
     if (n_tokens == 0) return FA_OK;
     if (!x || !weight || !out) return fail(FA_ERR_INVALID_ARG, "%s: null pointer argument", fn);
     if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
-    FA_HIP(fa::launch_rms_norm_quant(const_cast<uint16_t*>(x), nullptr, weight, eps, nullptr,
+    FA_HIP(fa::launch_rms_norm_quant(x, nullptr, nullptr, weight, eps, nullptr,
                                      nullptr, dim, 1, nullptr, nullptr,
                                      out, n_tokens, dim, (hipStream_t)stream));
     return FA_OK;
@@ -877,7 +872,7 @@ int fa_rms_norm_quant(const uint16_t* x, const uint16_t* weight, float eps,
     if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
     const int g = eff_group(dim, group_size);
     const int G = (dim + g - 1) / g;
-    FA_HIP(fa::launch_rms_norm_quant(const_cast<uint16_t*>(x), nullptr, weight, eps, smooth_inv,
+    FA_HIP(fa::launch_rms_norm_quant(x, nullptr, nullptr, weight, eps, smooth_inv,
                                      act_scale, g, G, X_q, X_scale, out,
                                      n_tokens, dim, (hipStream_t)stream));
     return FA_OK;
@@ -897,7 +892,7 @@ int fa_residual_rms_norm_quant(uint16_t* h, const uint16_t* resid, const uint16_
     if (dim > 65536) return fail(FA_ERR_INVALID_ARG, "%s: dim=%d exceeds 65536", fn, dim);
     const int g = eff_group(dim, group_size);
     const int G = (dim + g - 1) / g;
-    FA_HIP(fa::launch_rms_norm_quant(h, resid, weight, eps, smooth_inv, act_scale, g, G, X_q,
+    FA_HIP(fa::launch_rms_norm_quant(h, resid, h, weight, eps, smooth_inv, act_scale, g, G, X_q,
                                      X_scale, out, n_tokens, dim, (hipStream_t)stream));
     return FA_OK;
 }

@@ -107,8 +107,10 @@ hipError_t launch_quantize_activations(const uint16_t* X, const uint16_t* up, Pr
                                        int8_t* x_q, float* x_scale, uint16_t* out_f16,
                                        int N, int K, int g, int G, hipStream_t stream);
 
-// resid non-null: x <- fp16(x + resid) in place first (residual add fused).
-hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint16_t* weight,
+// Normalises h = fp16(x + resid) (resid non-null; h_out required) or h = x,
+// storing h to h_out when non-null (h_out == x updates x in place).
+hipError_t launch_rms_norm_quant(const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                                 const uint16_t* weight,
                                  float eps,
                                  const uint16_t* smooth_inv, const uint16_t* act_scale,
                                  int g, int G, int8_t* x_q, float* x_scale, uint16_t* out_f16,

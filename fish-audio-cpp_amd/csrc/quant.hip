@@ -203,7 +203,7 @@ int lanes_log2_for(int g, int vec) {
 // sums are reduced by the same tree.  rsqrtf is replaced by a double 1/sqrt.
 // The normalised fp16 row is then quantized per K-group straight from LDS.
 __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
-    uint16_t* __restrict__ x, const uint16_t* __restrict__ resid,
+    const uint16_t* x, const uint16_t* __restrict__ resid, uint16_t* h_out,
     const uint16_t* __restrict__ weight, float eps,
     const uint16_t* __restrict__ smooth_inv, const uint16_t* __restrict__ act_scale,
     int8_t* __restrict__ x_q, float* __restrict__ x_scale, uint16_t* __restrict__ out_f16,
@@ -217,8 +217,10 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
     // Thread t holds x[t], x[t + T], ... (at most kNV of them when
     // dim <= kNV * T, else the loop re-reads x); all its loads, gamma's
     // included, go out before the first use, so the row costs one memory
-    // latency.  With `resid`, x is first replaced by fp16(x + resid) in
-    // place (residual_add, ffn_activations.cu:41-45).
+    // latency.  With `resid` the row normalised is h = fp16(x + resid)
+    // (residual_add, ffn_activations.cu:41-45), else h = x; h is stored to
+    // h_out when h_out is non-null (required with resid; h_out may equal x,
+    // an in-place update).
     constexpr int kNV = 8;
     const bool regs = dim <= kNV * T;
     float xv[kNV], gv[kNV];
@@ -234,18 +236,20 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
 #pragma unroll
         for (int j = 0; j < kNV; ++j) {
             xv[j] = h2f(xr[j]);
+            uint16_t hs = xr[j];
             if (resid) {
-                const uint16_t hs = f2h(xv[j] + h2f(rr[j]));
+                hs = f2h(xv[j] + h2f(rr[j]));
                 xv[j] = h2f(hs);
-                if (tid < T && tid + j * T < dim) x[base + tid + j * T] = hs;
             }
+            if (h_out && tid < T && tid + j * T < dim) h_out[base + tid + j * T] = hs;
             gv[j] = h2f(gr[j]);
         }
-    } else if (resid) {
+    } else if (h_out) {
         for (int i = tid; i < dim; i += blockDim.x)
-            x[base + i] = f2h(h2f(x[base + i]) + h2f(resid[base + i]));
+            h_out[base + i] = resid ? f2h(h2f(x[base + i]) + h2f(resid[base + i])) : x[base + i];
         __syncthreads();
     }
+    const uint16_t* hrow = resid ? h_out : x;  // h, where the re-reading paths find it
 
     float local = 0.0f;
     if (tid < T) {
@@ -255,7 +259,7 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
                 if (tid + j * T < dim) local = __builtin_fmaf(xv[j], xv[j], local);
         } else {
             for (int i = tid; i < dim; i += T) {
-                float v = h2f(x[base + i]);
+                float v = h2f(hrow[base + i]);
                 local = __builtin_fmaf(v, v, local);
             }
         }
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(1024) void rms_norm_quant_kernel(
         }
     } else {
         for (int i = tid; i < dim; i += blockDim.x) {
-            uint16_t h = f2h((h2f(x[base + i]) * r) * h2f(weight[i]));
+            uint16_t h = f2h((h2f(hrow[base + i]) * r) * h2f(weight[i]));
             s_row[i] = h;
             if (out_f16) out_f16[base + i] = h;
         }
@@ -454,7 +458,8 @@ hipError_t launch_quantize_activations(const uint16_t* X, const uint16_t* up, Pr
     return hipGetLastError();
 }
 
-hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint16_t* weight,
+hipError_t launch_rms_norm_quant(const uint16_t* x, const uint16_t* resid, uint16_t* h_out,
+                                 const uint16_t* weight,
                                  float eps,
                                  const uint16_t* smooth_inv, const uint16_t* act_scale,
                                  int g, int G, int8_t* x_q, float* x_scale, uint16_t* out_f16,
@@ -467,8 +472,9 @@ hipError_t launch_rms_norm_quant(uint16_t* x, const uint16_t* resid, const uint1
                       ((uintptr_t)x_q & 7) == 0;
     const int lg = x_q ? lanes_log2_for(g, vec8 ? 8 : 1) : 0;
     const size_t lds = ((size_t)dim * 2 + 15) & ~(size_t)15;
+    if (resid && !h_out) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(n_tokens), dim3(block), lds, stream, x, resid,
-                       weight, eps, smooth_inv, act_scale, x_q, x_scale, out_f16, dim, T, g, G, lg,
+                       h_out, weight, eps, smooth_inv, act_scale, x_q, x_scale, out_f16, dim, T, g, G, lg,
                        vec8 ? 1 : 0);
     return hipGetLastError();
 }
