@@ -4,7 +4,10 @@
 // Dispatch for the linear layer (reference dispatcher: int8_gemm.cu:384-511):
 //   16-byte aligned W and X_q, N <= 16 and a shape plan_gemv takes:
 //       N == 1        -> v_dot4 GEMV, one wave per 1-2 weight rows (gemv.hip)
-//       2 <= N <= 16  -> int8 MFMA GEMV, 16-row tiles (gemv.hip)
+//       2 <= N <= 16  -> int8 MFMA GEMV, 16-row tiles (gemv.hip); fa_w8a8_gemm
+//                        lets it quantize the fp16 tokens itself when the
+//                        shape allows, and fa_w8a8_gemm_swiglu lets its
+//                        epilogue form the SwiGLU pairs
 //   aligned, K % 64 == 0, group % 64 == 0 -> LDS-tiled int8 MFMA GEMM (gemm.hip)
 //   anything else -> the exact any-shape kernel (gemm.hip, generic)
 // All paths sum the K-groups in the same order, so they agree bit for bit.
@@ -385,6 +388,16 @@ static int gemm_impl(const int8_t* W, const uint16_t* w_scale, int group_size,
             return FA_OK;
         }
     }
+    if (N >= 2 && N <= 16 && aligned16_or_null(smooth_inv) && aligned16(W) && aligned16(X)) {
+        // small batch: the MFMA GEMV quantizes the tokens itself when the
+        // wave's K range fits its registers
+        fa::GemvPlan gp = fa::plan_gemv(M, N, K, g, G, true, 0, 0, smooth_inv != nullptr);
+        if (gp.kind == 3) {
+            FA_HIP(fa::launch_gemv(gp, W, w_scale, nullptr, nullptr, X, act_scale, smooth_inv, Y,
+                                   nullptr, 0, 0, 0, 0, M, N, K, g, G, s));
+            return FA_OK;
+        }
+    }
     Workspace* ws = nullptr;
     rc = current_ws(&ws);
     if (rc) return rc;
@@ -597,6 +610,43 @@ static int gemm_swiglu_impl(const int8_t* W13, const uint16_t* w13_scale, int gr
                                    resid ? h_out : nullptr));
             if (!resid && h_out)
                 FA_HIP(hipMemcpyAsync(h_out, x, nk * 2, hipMemcpyDeviceToDevice, s));
+            return FA_OK;
+        }
+    }
+    if (N >= 2 && N <= 16 && aligned16(W13)) {
+        // small batch: the MFMA GEMV's epilogue forms the pairs; without the
+        // RMSNorm it also quantizes the tokens when their range fits
+        fa::GemvPlan gp{};
+        if (!gamma && aligned16(x) && aligned16_or_null(smooth_inv))
+            gp = fa::plan_gemv(M, N, K, g, G, true, 0, 1, smooth_inv != nullptr);
+        if (gp.kind == 3) {
+            FA_HIP(fa::launch_gemv(gp, W13, w13_scale, nullptr, nullptr, x, act_scale, smooth_inv,
+                                   act, nullptr, 0, 0, 0, 0, M, N, K, g, G, s));
+            return FA_OK;
+        }
+        gp = fa::plan_gemv(M, N, K, g, G, false, 0, 1);
+        if (gp.kind == 3) {
+            Workspace* ws = nullptr;
+            rc = current_ws(&ws);
+            if (rc) return rc;
+            void* p = ws->xq;
+            rc = grow(&p, &ws->xq_bytes, nk, s);
+            ws->xq = (int8_t*)p;
+            if (rc) return rc;
+            p = ws->xs;
+            rc = grow(&p, &ws->xs_bytes, (size_t)N * (size_t)G * sizeof(float), s);
+            ws->xs = (float*)p;
+            if (rc) return rc;
+            if (gamma)
+                FA_HIP(fa::launch_rms_norm_quant(x, resid, h_out, gamma, eps, smooth_inv,
+                                                 act_scale, g, G, ws->xq, ws->xs, nullptr, N, K,
+                                                 s));
+            else
+                FA_HIP(fa::launch_quantize_activations(x, nullptr, fa::Prologue::kPlain,
+                                                       act_scale, smooth_inv, ws->xq, ws->xs,
+                                                       nullptr, N, K, g, G, s));
+            FA_HIP(fa::launch_gemv(gp, W13, w13_scale, ws->xq, ws->xs, nullptr, nullptr, nullptr,
+                                   act, nullptr, 0, 0, 0, 0, M, N, K, g, G, s));
             return FA_OK;
         }
     }

@@ -142,17 +142,22 @@ struct GemvPlan {
     bool lc = false; // mfma: all terms in LDS, one chain lane per output
     int pro = 0;     // dot with in-kernel quantization: fused prologue (0 plain,
                      // 1 SiLU*mul, 2 residual + RMSNorm)
-    int epi = 0;     // dot: 1 = SwiGLU pair epilogue (rows interleaved w1 / w3),
-                     // 2 = the same on separate w1 / w3 quantized apart
+    int epi = 0;     // 1 = SwiGLU pair epilogue (rows interleaved w1 / w3; dot and
+                     // mfma), 2 = the same on separate w1 / w3 quantized apart (dot)
+    int qx = 0;      // mfma: quantizes the fp16 tokens in-kernel (1; 2 with smooth_inv)
     int grid = 0, block = 0;
     size_t lds = 0;
 };
-// qx: the dot kernel quantizes the fp16 token itself (N == 1 only); pro != 0
-// adds a fused prologue in front of that quantizer (N == 1, K <= 12288,
-// K % 8 == 0), else the plan is empty.
-// epi == 1 plans the SwiGLU pair epilogue (two rows per wave, M even,
-// pro 0 or 2): Y [M / 2] gets fp16(fp16(silu(row 2i)) * row 2i+1).
-GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0);
+// qx: the kernel quantizes the fp16 tokens itself (N == 1: the dot kernel;
+// 2 <= N <= 16: the MFMA kernel when the wave's K range fits its registers,
+// `smooth` telling whether a smooth_inv vector comes along), else the plan is
+// empty; pro != 0 adds a fused prologue in front of that quantizer (N == 1,
+// K <= 12288, K % 8 == 0).
+// epi == 1 plans the SwiGLU pair epilogue (M even; N == 1: two rows per
+// wave, pro 0 or 2; N > 1: staged or in-kernel quantized tokens): Y [N][M / 2]
+// gets fp16(fp16(silu(row 2i)) * row 2i+1).
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0,
+                   bool smooth = false);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
 // [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to

@@ -10,10 +10,6 @@ namespace fa {
 using namespace gv;
 namespace {
 
-template <bool D>
-using MfmaFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*, uint16_t*,
-                        DbgWindow, int, int, int, int);
-
 template <int SPG, bool LC, bool D>
 MfmaFn<D> mfma_for_maxg(int maxg) {
     switch (maxg) {
@@ -66,10 +62,12 @@ int device_cus() {
     return n;
 }
 
-GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi) {
+GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi, bool smooth) {
     GemvPlan p{};
     if (pro != 0 && (!qx || N != 1 || K > 3 * 8 * 64 * kDotWavesQx || K % 8 != 0)) return p;
-    if (epi != 0 && (!qx || N != 1 || pro == 1 || (M & 1))) return p;
+    if (epi != 0 && (M & 1)) return p;
+    if (epi != 0 && N == 1 && (!qx || pro == 1)) return p;
+    if (epi == 2 && N != 1) return p;
     if (N == 1 && (g == 64 || g == 128 || g == 256 || g == 512) && K % 16 == 0 && K <= 32768) {
         const int lgroups = g / 16;
         // rows per wave (measured on MI355X over the layer shapes at g256):
@@ -116,6 +114,14 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi)
         if (nw < ceil_div(G, 20)) nw = ceil_div(G, 20);
         if (nw > G) nw = G;
         if (nw > 8) nw = 8;
+        const int qx_lim = smooth ? kMfmaQxStepsSmooth : kMfmaQxSteps;
+        if (qx) {
+            // in-kernel quantization holds the wave's fp16 values (8 VGPRs a
+            // step, 16 with smooth_inv) until they become codes: more waves
+            // per tile when the range is too long
+            while (nw < 8 && nw < G && (g / 64) * round_maxg(ceil_div(G, nw)) > qx_lim) ++nw;
+            if ((g / 64) * round_maxg(ceil_div(G, nw)) > qx_lim) return GemvPlan{};
+        }
         if (ceil_div(G, nw) > 20) return GemvPlan{};
         p.kind = 3;
         p.spg = g / 64;
@@ -127,6 +133,8 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi)
         p.lc = tiles < 384 && lds_lc <= 64 * 1024;
         p.lds = p.lc ? lds_lc : (size_t)(2 * kTile * G + kTile * kTile) * sizeof(float);
         if (p.lds > 64 * 1024) return GemvPlan{};
+        p.epi = epi;
+        if (qx) p.qx = smooth ? 2 : 1;
         return p;
     }
     return GemvPlan{};
@@ -162,14 +170,22 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
         hipLaunchKernelGGL(fn, dim3(grid), dim3(p.block), p.lds, stream, W, w_scale, x_q, x_scale,
                            X, act_scale, smooth_inv, Y, dbg, M, K, p.lg, G, p.passes, p.grid, pro);
     } else if (p.kind == 3) {
-        if (X || p.pro) return hipErrorInvalidValue;
+        if (p.pro || (p.qx != 0) != (X != nullptr)) return hipErrorInvalidValue;
+        if ((p.qx == 2) != (smooth_inv != nullptr)) return hipErrorInvalidValue;
+        if (p.epi && (M & 1)) return hipErrorInvalidValue;
         const bool d = dbg_partials != nullptr;
-        if (d)
+        if (d && (p.qx || p.epi)) return hipErrorInvalidValue;   // debug window: staged codes
+        if (d) {
             hipLaunchKernelGGL(mfma_for<true>(p.lc, p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
-                               stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
-        else
-            hipLaunchKernelGGL(mfma_for<false>(p.lc, p.spg, p.maxg), dim3(p.grid), dim3(p.block), p.lds,
-                               stream, W, w_scale, x_q, x_scale, Y, dbg, M, N, K, G);
+                               stream, W, w_scale, x_q, x_scale, X, act_scale, smooth_inv, Y, dbg,
+                               M, N, K, G);
+        } else {
+            MfmaFn<false> fn = (p.qx || p.epi) ? mfma_fused(p.qx, p.epi, p.lc, p.spg, p.maxg)
+                                               : mfma_for<false>(p.lc, p.spg, p.maxg);
+            if (!fn) return hipErrorInvalidValue;
+            hipLaunchKernelGGL(fn, dim3(p.grid), dim3(p.block), p.lds, stream, W, w_scale, x_q,
+                               x_scale, X, act_scale, smooth_inv, Y, dbg, M, N, K, G);
+        }
     } else {
         return hipErrorInvalidValue;
     }

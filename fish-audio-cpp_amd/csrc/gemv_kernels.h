@@ -31,6 +31,14 @@
 // over 64 bytes; g/64 chained MFMAs make P_g.  Terms are kept in registers;
 // afterwards the waves pass the running fp32 sums along in group order
 // through LDS.
+//
+// With QX the MFMA kernel quantizes the fp16 tokens itself: lane l loads the
+// 16 fp16 values of token l&15 that its B fragment covers at every step of
+// the wave's K range, the group maximum comes from its own values and the
+// three other lanes of the same token (xor 16, 32), and the codes go straight
+// into the hoisted B fragments; no int8 copy of the tokens is written.  With
+// EPI 1 rows 2i / 2i+1 are a SwiGLU pair (gate, up) and Y [N][M / 2] gets
+// fp16(fp16(silu(fp16(gate))) * fp16(up)).
 #pragma once
 
 #include "common.h"
@@ -551,12 +559,22 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
 
 constexpr int kTile = 16;
 
-template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0, int kKD = 12>
+__device__ __forceinline__ uint16_t swiglu_h(uint16_t gate, uint16_t up) {
+    return f2h(h2f(f2h(silu_f(h2f(gate)))) * h2f(up));
+}
+
+// QX: 0 = staged int8 codes (x_q, x_scale), 1 = quantize X in-kernel,
+// 2 = the same times smooth_inv.  EPI 1: SwiGLU pairs (M even).
+template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0, int kKD = 12, int QX = 0,
+          int EPI = 0>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
     const int8_t* __restrict__ x_q, const float* __restrict__ x_scale,
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ act_scale,
+    const uint16_t* __restrict__ smooth_inv,
     uint16_t* __restrict__ Y, DbgWindow dbg, int M, int N, int K, int G) {
     constexpr int NSTEP = SPG * MAXG;
+    static_assert(QX == 0 || NSTEP <= 32, "in-kernel quantization fills the hoisted codes");
     // ring depth: kKD steps, 8 when 16+ groups' terms are held in registers
     constexpr int KDM = (!LC && MAXG >= 16) ? 8 : kKD;
     constexpr int KD = NSTEP < KDM ? NSTEP : KDM;
@@ -586,7 +604,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const size_t kbase = (size_t)gb * SPG * 64 + kq;
     const int8_t* wp = W + (size_t)row_ld * K + kbase;
     // token lanes past N read token N-1: their MFMA columns are never stored
-    const int8_t* xp = x_q + (size_t)min(lr, N - 1) * K + kbase;
+    const int8_t* xp = QX ? nullptr : x_q + (size_t)min(lr, N - 1) * K + kbase;
 
     // The wave's B fragments (the tokens' codes of its K range) are loaded
     // once, ahead of the weight ring, when they fit in registers (measured
@@ -597,7 +615,27 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     v4i a[KD], b[BH ? 1 : KD];
     v4i bh[BH ? NSTEP : 1];
     const v4i zero = {0, 0, 0, 0};
-    if constexpr (BH) {
+    // QX: the 16 fp16 values per step (two 16-byte chunks), the smooth_inv
+    // chunks (QX 2) and the static group scales, loaded first
+    v4i xf[QX ? NSTEP : 1][2], sf[QX == 2 ? NSTEP : 1][2];
+    uint16_t asr[QX ? MAXG : 1];
+    if constexpr (QX) {
+        const uint16_t* xh = X + (size_t)min(lr, N - 1) * K + kbase;
+#pragma unroll
+        for (int st = 0; st < NSTEP; ++st) {
+            const size_t off = (size_t)(st < nvalid ? st : 0) * 64;
+            xf[st][0] = *reinterpret_cast<const v4i*>(xh + off);
+            xf[st][1] = *reinterpret_cast<const v4i*>(xh + off + 8);
+            if constexpr (QX == 2) {
+                sf[st][0] = *reinterpret_cast<const v4i*>(smooth_inv + kbase + off);
+                sf[st][1] = *reinterpret_cast<const v4i*>(smooth_inv + kbase + off + 8);
+            }
+        }
+        // without static scales these loads re-read w_scale (not used)
+        const uint16_t* asp = act_scale ? act_scale : w_scale;
+#pragma unroll
+        for (int j = 0; j < MAXG; ++j) asr[j] = asp[gb + (j < ng ? j : 0)];
+    } else if constexpr (BH) {
 #pragma unroll
         for (int st = 0; st < NSTEP; ++st)
             bh[st] = ld16(xp + (size_t)(st < nvalid ? st : 0) * 64);
@@ -624,16 +662,71 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
         const int r = i / G, gi = i - r * G;
         const int row = min(row0 + r, M - 1);
         wsr[q] = w_scale[G == 1 ? (size_t)row : (size_t)row * G + gi];
-        xsr[q] = x_scale[(size_t)min(r, N - 1) * G + gi];
+        if constexpr (!QX) xsr[q] = x_scale[(size_t)min(r, N - 1) * G + gi];
     }
 #pragma unroll
     for (int s = 0; s < KD; ++s) load(s, s);
+    // QX: per (token lr, group) scale (int8_gemm.cu:147-211 semantics: the
+    // group's |v| maximum / 127 or the static scale, clamped at 1e-8) and the
+    // codes rint(v / s) clipped to +-127, packed in memory byte order
+    float qsv[QX ? MAXG : 1];
+    if constexpr (QX) {
+        // value e of step st, formed from the packed halves where it is used
+        // (no float copy of the wave's values stays live)
+        auto val = [&](int st, int e) {
+            const int w = xf[st][e >> 3][(e >> 1) & 3];
+            float x = h2f((uint16_t)((e & 1) ? ((unsigned)w >> 16) : ((unsigned)w & 0xffffu)));
+            if constexpr (QX == 2) {
+                const int sw = sf[st][e >> 3][(e >> 1) & 3];
+                x *= h2f((uint16_t)((e & 1) ? ((unsigned)sw >> 16) : ((unsigned)sw & 0xffffu)));
+            }
+            return x;
+        };
+#pragma unroll
+        for (int j = 0; j < MAXG; ++j) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) {
+                const int st = j * SPG + s;
+                float m = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(val(st, e)));
+                amax = st < nvalid ? fmaxf(amax, m) : amax;
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            float sc;
+            if (act_scale) {
+                sc = h2f(asr[j]);
+                sc = sc < 1e-8f ? 1e-8f : sc;
+            } else {
+                sc = act_scale_from_amax(amax);
+            }
+            qsv[j] = sc;
+            const float inv = 1.0f / sc;
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) {
+                const int st = j * SPG + s;
+                v4i c;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    unsigned u = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        u |= ((unsigned)quant_rn(val(st, 4 * d + b), inv) & 0xffu) << (8 * b);
+                    c[d] = (int)u;
+                }
+                bh[st] = c;
+            }
+            if (LC && lane < 16 && j < ng) xs_s[lr * G + gb + j] = sc;
+        }
+    }
 #pragma unroll
     for (int q = 0; q < kSt; ++q) {
         const int i = threadIdx.x + q * blockDim.x;
         if ((kAb & 4) == 0 && i < kTile * G) {
             ws_s[i] = h2f(wsr[q]);
-            xs_s[i] = xsr[q];
+            if constexpr (!QX) xs_s[i] = xsr[q];
         }
     }
     __syncthreads();
@@ -680,33 +773,49 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     if constexpr (LC) {
         // one lane per output runs the whole chain in group order
         __syncthreads();
-        for (int t = threadIdx.x; t < kTile * N; t += blockDim.x) {
-            const int r = t & (kTile - 1), tok = t >> 4;
+        // (EPI 1: one lane per SwiGLU pair runs both rows' chains)
+        constexpr int RPL = EPI == 1 ? 2 : 1;   // rows per lane
+        for (int t = threadIdx.x; t < kTile / RPL * N; t += blockDim.x) {
+            const int r = (t & (kTile / RPL - 1)) * RPL, tok = t / (kTile / RPL);
             const float* tp = tl + tok * kTile + r;      // term of group gi at gi * ns * kTile
             const float* xp = xs_s + tok * G;
-            float acc = 0.0f;
+            float acc[RPL] = {};
             // eight groups' operands read before their eight fmas, so the
             // chain waits on LDS once per eight groups, not once per group
             int gi = 0;
             for (; gi + 8 <= G; gi += 8) {
-                float tv[8], xv[8];
+                float tv[8][RPL], xv[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    tv[u] = tp[(gi + u) * ns * kTile];
+#pragma unroll
+                    for (int q = 0; q < RPL; ++q) tv[u][q] = tp[(gi + u) * ns * kTile + q];
                     xv[u] = xp[gi + u];
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(tv[u], xv[u], acc);
+                for (int u = 0; u < 8; ++u)
+#pragma unroll
+                    for (int q = 0; q < RPL; ++q) acc[q] = __builtin_fmaf(tv[u][q], xv[u], acc[q]);
             }
-            for (; gi < G; ++gi) acc = __builtin_fmaf(tp[gi * ns * kTile], xp[gi], acc);
-            if (row0 + r < M) Y[(size_t)tok * M + row0 + r] = f2h(acc);
+            for (; gi < G; ++gi)
+#pragma unroll
+                for (int q = 0; q < RPL; ++q)
+                    acc[q] = __builtin_fmaf(tp[gi * ns * kTile + q], xp[gi], acc[q]);
+            if (row0 + r < M) {
+                if constexpr (EPI == 1)
+                    Y[(size_t)tok * (M >> 1) + ((row0 + r) >> 1)] = swiglu_h(f2h(acc[0]), f2h(acc[1]));
+                else
+                    Y[(size_t)tok * M + row0 + r] = f2h(acc[0]);
+            }
         }
     } else {
         // this lane's token scales for the wave's groups, read before the chain
         // (the chain's LDS writes would otherwise keep these reads inside it)
         float xsv[MAXG];
 #pragma unroll
-        for (int j = 0; j < MAXG; ++j) xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
+        for (int j = 0; j < MAXG; ++j) {
+            if constexpr (QX) xsv[j] = qsv[j];
+            else xsv[j] = xs_s[lr * G + gb + (j < ng ? j : 0)];
+        }
 
         // Group-ordered fp32 chain: wave 0 starts from zero, each wave continues
         // the previous wave's sums over its own groups.
@@ -723,12 +832,36 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
             }
             __syncthreads();
         }
-        for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
-            const int t = i / kTile, r = i - t * kTile;
-            if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
+        if constexpr (EPI == 1) {
+            for (int i = threadIdx.x; i < kTile / 2 * N; i += blockDim.x) {
+                const int t = i / (kTile / 2), r = 2 * (i - t * (kTile / 2));
+                if (row0 + r < M)
+                    Y[(size_t)t * (M >> 1) + ((row0 + r) >> 1)] =
+                        swiglu_h(f2h(chain[t * kTile + r]), f2h(chain[t * kTile + r + 1]));
+            }
+        } else {
+            for (int i = threadIdx.x; i < kTile * N; i += blockDim.x) {
+                const int t = i / kTile, r = i - t * kTile;
+                if (row0 + r < M) Y[(size_t)t * M + row0 + r] = f2h(chain[t * kTile + r]);
+            }
         }
     }
 }
+
+template <bool D>
+using MfmaFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*,
+                        const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,
+                        int, int, int, int);
+
+// Steps (64 bytes of K) a wave may hold as fp16 for in-kernel quantization
+// (the largest counts that compile without scratch spills for gfx950).
+constexpr int kMfmaQxSteps = 16;
+constexpr int kMfmaQxStepsSmooth = 8;
+
+// The MFMA kernel with in-kernel quantization (qx 1 plain, 2 smooth_inv)
+// and / or the SwiGLU pair epilogue (epi 1); null for a shape outside the
+// instantiated set (gemv_mfma_fused.hip).
+MfmaFn<false> mfma_fused(int qx, int epi, bool lc, int spg, int maxg);
 
 using DotFn = void (*)(const int8_t*, const uint16_t*, const int8_t*, const float*,
                        const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, DbgWindow,

@@ -29,7 +29,7 @@ HIP_FLAGS = [
     "-Wall",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemv.hip", "gemv_dot.hip", "gemv_dot_pro.hip", "gemv_dot_swiglu.hip",
+HIP_SOURCES = ["quant.hip", "gemv.hip", "gemv_dot.hip", "gemv_dot_pro.hip", "gemv_dot_swiglu.hip", "gemv_mfma_fused.hip",
                "gemv_f16.hip", "gemm.hip", "chain.hip", "attn.hip"]
 HOST_SOURCES = ["api.cpp", "loader.cpp", "kernels_cxx.cpp"]
 

@@ -386,6 +386,33 @@ def test_static_and_smooth_through_entry_point():
     assert same(host(Y), ref.w8a8_gemm(q, s, g, x, act_scale=act, smooth_inv=sm)), "static"
 
 
+@pytest.mark.parametrize("N,M,K,g", [
+    (8, 2560, 4096, 64),    # configs[2] o: in-kernel quantization, terms in LDS
+    (8, 6144, 2560, 64),    # configs[2] qkv: more waves per tile so the range fits
+    (8, 2560, 9728, 64),    # configs[2] down: range too long, separate quantizer
+    (3, 333, 1344, 256),    # K % g != 0: the last group one 64-byte step
+    (16, 48, 512, 512),     # one group of eight steps
+    (2, 100, 192, 128),     # two groups, the second short
+    (13, 1000, 2560, 256),
+])
+@pytest.mark.parametrize("mode", ["dynamic", "static", "smooth", "static_smooth"])
+def test_small_batch_entry_quantization(N, M, K, g, mode):
+    """fa_w8a8_gemm at 2 <= N <= 16, where the MFMA GEMV quantizes the fp16
+    tokens itself (or the separate quantizer runs when the wave's K range is
+    too long): Y equals the oracle's quantize-then-linear for dynamic and
+    static scales, with and without smooth_inv."""
+    print("qx N=%d M=%d K=%d g=%d %s" % (N, M, K, g, mode), flush=True)
+    q, s = make_linear(M, K, g, seed=M + K)
+    x = synth.activations_f16(N, K, seed=N + K)
+    G = (K + g - 1) // g
+    act = np.full(G, 0.03, np.float16) if "static" in mode else None
+    sm = synth.gamma_f16(K, seed=K + 1) if "smooth" in mode else None
+    Y = ops.w8a8_gemm(dev(q), dev(s), dev(x), g,
+                      act_scale=None if act is None else dev(act),
+                      smooth_inv=None if sm is None else dev(sm))
+    assert same(host(Y), ref.w8a8_gemm(q, s, g, x, act_scale=act, smooth_inv=sm)), mode
+
+
 def test_gemv_deterministic_across_calls():
     """Repeated calls with other shapes in between give identical Y."""
     K, Nout = LAYER["down"]
@@ -526,7 +553,7 @@ def test_gemm_rms_small_and_odd_dims():
         assert same(host(Y), ref.gemm_quantized(q, s_, g, rq, rs)), K
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 8, 16])
 @pytest.mark.parametrize("g", [256, 64])
 @pytest.mark.parametrize("mode", ["rms_resid", "rms", "plain"])
 def test_gemm_swiglu_bitexact(g, T, mode):
