@@ -345,6 +345,21 @@ int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size) {
     return fa::gemm_tile_split(M, N, K, g, fa::gemm_tile_choice(M, N, K, g));
 }
 
+int fa_debug_gemv_plan(int M, int N, int K, int group_size, int qx, int pro, int epi,
+                       int smooth, int* out) {
+    g_err.clear();
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int g = eff_group(K, group_size);
+    const int G = (K + g - 1) / g;
+    const fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G, qx != 0, pro, epi, smooth != 0);
+    if (out) {
+        out[0] = p.kind; out[1] = p.grid; out[2] = p.block; out[3] = (int)p.lds;
+        out[4] = p.spg; out[5] = p.maxg; out[6] = p.lc ? 1 : 0; out[7] = p.qx; out[8] = p.epi;
+        out[9] = p.kind ? (fa::gemv_plan_valid(p, M, N, K, g, G) ? 1 : 0) : 0;
+    }
+    return p.kind;
+}
+
 int fa_w8a8_gemm_partials(const int8_t* W, const uint16_t* w_scale, int group_size,
                           const int8_t* X_q, const float* X_scale, uint16_t* Y, int32_t* partials,
                           int row0, int rows, int tok0, int toks, int M, int N, int K,

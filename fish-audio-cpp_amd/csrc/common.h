@@ -158,6 +158,9 @@ struct GemvPlan {
 // gets fp16(fp16(silu(row 2i)) * row 2i+1).
 GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0,
                    bool smooth = false);
+// The grid and shape assumptions of the decode kernels, checked by
+// launch_gemv before every launch (a plan that fails them is refused).
+bool gemv_plan_valid(const GemvPlan& p, int M, int N, int K, int g, int G);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
 // [dbg_tok0, +dbg_toks) x [dbg_row0, +dbg_rows) to

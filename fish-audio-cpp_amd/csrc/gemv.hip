@@ -140,6 +140,42 @@ GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi,
     return GemvPlan{};
 }
 
+bool gemv_plan_valid(const GemvPlan& p, int M, int N, int K, int g, int G) {
+    // What the kernels take for granted about their grid and shapes; a plan
+    // outside it is a planning bug and is refused before any launch.
+    if (M <= 0 || N <= 0 || K <= 0 || g <= 0 || G != ceil_div(K, g)) return false;
+    if (p.block <= 0 || p.block % 64 != 0 || p.grid <= 0) return false;
+    if (p.kind == 1 || p.kind == 2) {
+        const int R = p.kind;
+        const int nwv = p.block / 64;
+        if (N != 1 || (nwv != kDotWaves && nwv != kDotWavesQx)) return false;
+        if (g != 64 && g != 128 && g != 256 && g != 512) return false;
+        if ((1 << p.lg) != g || g / 16 > 64 / R) return false;      // a group fits a row's lanes
+        if (K % 16 != 0 || K > 32768) return false;
+        if (p.passes != ceil_div(K, (64 / R) * 16)) return false;
+        if (p.kd < 3 || p.kd > 5) return false;
+        if ((long long)p.grid * nwv * R < M) return false;         // every row has a wave
+        if (p.pro != 0 && K > 3 * 8 * 64 * kDotWavesQx) return false;
+        if (p.epi != 0 && (R != 2 || (M & 1))) return false;
+        return p.lds <= 64 * 1024;
+    }
+    if (p.kind == 3) {
+        const int nw = p.block / 64;
+        if (N > 16 || nw > 8 || K % 64 != 0 || p.spg * 64 != g) return false;
+        if (p.spg != 1 && p.spg != 2 && p.spg != 4 && p.spg != 8) return false;
+        if (p.grid != ceil_div(M, kTile)) return false;
+        if (ceil_div(G, nw) > p.maxg || p.maxg > 20 || nw > G) return false;  // each wave's groups
+        if (kTile * G > 5 * p.block) return false;                // scale staging: 5 per thread
+        if (p.qx && p.spg * p.maxg > (p.qx == 2 ? kMfmaQxStepsSmooth : kMfmaQxSteps)) return false;
+        if (p.epi != 0 && (p.epi != 1 || (M & 1))) return false;
+        const int ns = N <= 8 ? 8 : 16;
+        const size_t lds = p.lc ? (size_t)(2 * kTile * G + G * ns * kTile) * sizeof(float)
+                                : (size_t)(2 * kTile * G + kTile * kTile) * sizeof(float);
+        return p.lds == lds && p.lds <= 64 * 1024;
+    }
+    return false;
+}
+
 hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_scale,
                        const int8_t* x_q, const float* x_scale, const uint16_t* X,
                        const uint16_t* act_scale, const uint16_t* smooth_inv, uint16_t* Y,
@@ -150,6 +186,7 @@ hipError_t launch_gemv(const GemvPlan& p, const int8_t* W, const uint16_t* w_sca
                        const uint16_t* smooth_inv3) {
     DbgWindow dbg{dbg_partials, dbg_row0, dbg_rows, dbg_tok0, dbg_toks};
     const ProArgs pro{x2, gamma, h_out, eps, w3, w3_scale, act_scale3, smooth_inv3};
+    if (!gemv_plan_valid(p, M, N, K, g, G)) return hipErrorInvalidValue;
     if (p.kind == 1 || p.kind == 2) {
         const bool qx = X != nullptr;
         const int lgl = p.lg - 4;   // log2(lanes per group)

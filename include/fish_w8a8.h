@@ -168,6 +168,20 @@ int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_s
  * splits.) */
 int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size);
 
+/* Decode planning query with no reference counterpart (for tests and
+ * tools; no device call): the decode GEMV plan for N <= 16 tokens.  qx: the
+ * kernel quantizes fp16 tokens itself; pro: 0 plain, 1 SiLU*mul, 2 residual
+ * + RMSNorm prologue (one token); epi: 1 SwiGLU pairs, 2 separate w1 / w3;
+ * smooth: a smooth_inv vector comes along.  Returns the kernel kind (0: the
+ * shape takes another path; 1, 2: the one-token GEMV with 1 or 2 rows per
+ * wave; 3: the 2..16-token MFMA GEMV) and, when out is non-NULL, fills
+ * out[0..9] = kind, grid, block, LDS bytes, 64-byte steps per group, groups
+ * per wave, terms-in-LDS flag, in-kernel quantization (0/1/2), epilogue, and
+ * 1 if the plan meets the kernels' grid and shape assumptions (every launch
+ * checks this and refuses a plan that does not). */
+int fa_debug_gemv_plan(int M, int N, int K, int group_size, int qx, int pro, int epi,
+                       int smooth, int* out);
+
 /* Verification hook with no reference counterpart (the reference keeps its
  * int32 partials inside cuBLAS, int8_gemm.cu:476-488): runs exactly the kernel
  * fa_w8a8_gemm_quantized would run for this shape, writes Y, and also writes
