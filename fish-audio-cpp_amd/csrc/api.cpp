@@ -337,6 +337,10 @@ int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_s
                             (hipStream_t)stream);
 }
 
+int fa_w8a8_set_k_split(int max_splits) { return fa::set_k_split(max_splits); }
+
+int fa_debug_gemv_plan_rejects(void) { return fa::gemv_plan_rejects(); }
+
 int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size) {
     g_err.clear();
     if (M <= 0 || N <= 16 || K <= 0) return 1;
@@ -351,7 +355,7 @@ int fa_debug_gemv_plan(int M, int N, int K, int group_size, int qx, int pro, int
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const int g = eff_group(K, group_size);
     const int G = (K + g - 1) / g;
-    const fa::GemvPlan p = fa::plan_gemv(M, N, K, g, G, qx != 0, pro, epi, smooth != 0);
+    const fa::GemvPlan p = fa::plan_gemv_raw(M, N, K, g, G, qx != 0, pro, epi, smooth != 0);
     if (out) {
         out[0] = p.kind; out[1] = p.grid; out[2] = p.block; out[3] = (int)p.lds;
         out[4] = p.spg; out[5] = p.maxg; out[6] = p.lc ? 1 : 0; out[7] = p.qx; out[8] = p.epi;

@@ -156,10 +156,17 @@ struct GemvPlan {
 // epi == 1 plans the SwiGLU pair epilogue (M even; N == 1: two rows per
 // wave, pro 0 or 2; N > 1: staged or in-kernel quantized tokens): Y [N][M / 2]
 // gets fp16(fp16(silu(row 2i)) * row 2i+1).
+// A plan that fails gemv_plan_valid is never returned: plan_gemv counts it
+// (gemv_plan_rejects) and returns kind 0, so the caller takes its other path.
 GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0,
                    bool smooth = false);
+// The planner itself, before that check (the planning query reports its
+// plan and whether the check passes).
+GemvPlan plan_gemv_raw(int M, int N, int K, int g, int G, bool qx, int pro = 0, int epi = 0,
+                       bool smooth = false);
+int gemv_plan_rejects();
 // The grid and shape assumptions of the decode kernels, checked by
-// launch_gemv before every launch (a plan that fails them is refused).
+// plan_gemv on every plan and again by launch_gemv before every launch.
 bool gemv_plan_valid(const GemvPlan& p, int M, int N, int K, int g, int G);
 // Debug window: when dbg_partials is non-null the kernels also write the exact
 // int32 partial of every (token, row, group) inside
@@ -210,6 +217,7 @@ int gemm_tile_choice(int M, int N, int K, int g);
 // the split needs gemm_tile_split_bytes of partial sums plus one zeroed int
 // counter per tile (left zeroed by every launch).
 int gemm_tile_split(int M, int N, int K, int g, int variant = 0);
+int set_k_split(int max_splits);   // process-wide cap; returns the previous one
 size_t gemm_tile_split_bytes(int M, int N, int variant, int nsplit);
 hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8_t* x_q,
                             const float* x_scale, float* tables, uint16_t* Y, int32_t* dbg_partials,

@@ -21,6 +21,8 @@
 //   the group's scales ride along with its first stage into LDS.
 #include "common.h"
 
+#include <atomic>
+
 #include <type_traits>
 
 namespace fa {
@@ -1134,24 +1136,36 @@ int gemm_tile_choice(int M, int N, int K, int g) {
     return (t256 >= 1024 || (K >= 8192 && t256 >= 128)) ? 1 : 2;
 }
 
+namespace {
+std::atomic<int> g_max_splits{1};
+}
+
+int set_k_split(int max_splits) {
+    if (max_splits < 1) max_splits = 1;
+    if (max_splits > 8) max_splits = 8;
+    return g_max_splits.exchange(max_splits);
+}
+
 int gemm_tile_split(int M, int N, int K, int g, int variant) {
-    // Grids with far fewer tiles than the device holds at once (the o and
-    // down projections at 512 tokens: 80 tiles of 128 x 128 for 256 CUs)
-    // split K over 3 to 8 workgroups per tile, in whole groups.  The fp32 sum
-    // is then formed per split and the splits' sums added in split order, so
-    // the fp16 output is within the reassociation bound of the reference's
-    // single group-ordered chain (int32 partials stay exact).
+    // Opt-in (set_k_split): grids with far fewer tiles than an MI355X holds
+    // at once (the o and down projections at 512 tokens: 80 tiles of
+    // 128 x 128) split K over 3 to max_splits workgroups per tile, in whole
+    // groups.  The fp32 sum is then formed per split and the splits' sums
+    // added in split order, so the fp16 output is within the reassociation
+    // bound of the reference's single group-ordered chain (int32 partials
+    // stay exact).  The split count depends on the shape only (a fixed
+    // 256-CU slot count), never on the device the call runs on.
+    const int cap = g_max_splits.load(std::memory_order_relaxed);
+    if (cap < 3) return 1;
     if (variant == 0) variant = gemm_tile_choice(M, N, K, g);
     if (variant != 2 || g < 128) return 1;   // (the g64 split build spills)
 
     const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
-    const int cus = device_cus();
-    if (cus <= 0) return 1;
-    const int slots = cus * 2;   // two 128 x 128 workgroups per CU
+    const int slots = 256 * 2;   // two 128 x 128 workgroups per CU
     if (tiles * 2 > slots) return 1;
     const int units = (K / 128) / (g >= 256 ? g / 128 : 1);
     int sp = slots / tiles;
-    if (sp > 8) sp = 8;
+    if (sp > cap) sp = cap;
     if (sp > units) sp = units;
     // (measured on MI355X at 512 tokens, g256: o 28.5 -> 25.3 us and down
     // 61.1 -> 36.1 us at 6 splits; 2 splits made qkv slower, 21.4 -> 27.9 us,

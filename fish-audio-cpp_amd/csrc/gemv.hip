@@ -62,7 +62,25 @@ int device_cus() {
     return n;
 }
 
+namespace {
+std::atomic<int> g_plan_rejects{0};
+}
+
 GemvPlan plan_gemv(int M, int N, int K, int g, int G, bool qx, int pro, int epi, bool smooth) {
+    // A plan outside the kernels' assumptions is a planning bug: it is
+    // counted and dropped (kind 0), so the caller takes its other path
+    // (separate quantizer, the prefill kernels) instead of failing.
+    GemvPlan p = plan_gemv_raw(M, N, K, g, G, qx, pro, epi, smooth);
+    if (p.kind != 0 && !gemv_plan_valid(p, M, N, K, g, G)) {
+        g_plan_rejects.fetch_add(1, std::memory_order_relaxed);
+        return GemvPlan{};
+    }
+    return p;
+}
+
+int gemv_plan_rejects() { return g_plan_rejects.load(std::memory_order_relaxed); }
+
+GemvPlan plan_gemv_raw(int M, int N, int K, int g, int G, bool qx, int pro, int epi, bool smooth) {
     GemvPlan p{};
     if (pro != 0 && (!qx || N != 1 || K > 3 * 8 * 64 * kDotWavesQx || K % 8 != 0)) return p;
     if (epi != 0 && (M & 1)) return p;

@@ -86,6 +86,8 @@ SIGNATURES = {
     "fa_w8a8_gemm_swiglu": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _f, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_quantized": (_i, [_p, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "fa_w8a8_gemm_k_splits": (_i, [_i, _i, _i, _i]),
+    "fa_w8a8_set_k_split": (_i, [_i]),
+    "fa_debug_gemv_plan_rejects": (_i, []),
     "fa_debug_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _p]),
     "fa_w8a8_gemm_partials": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
     "fa_quantize_activations": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _p]),

@@ -5,6 +5,7 @@ in libfish_w8a8.so.  Shapes follow the reference kernel API
 (src/kernels/kernels.h:242-259): W [M, K] int8, w_scale fp16 [M] or [M, G],
 X [N, K] fp16, returned Y is [N, M] fp16 (= the reference's col-major [M, N]).
 """
+import contextlib
 import ctypes
 import sys
 
@@ -51,8 +52,25 @@ def w8a8_gemm(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=No
 
 def k_splits(M, N, K, group_size):
     """fa_w8a8_gemm_k_splits: 1 when the linear keeps the reference's single
-    group-ordered fp32 chain (bit-exact), else the number of K splits."""
+    group-ordered fp32 chain (bit-exact; always, unless set_k_split opted in),
+    else the number of K splits."""
     return lib().fa_w8a8_gemm_k_splits(M, N, K, group_size)
+
+
+def set_k_split(max_splits):
+    """fa_w8a8_set_k_split: opt in to (>= 3) or out of (<= 1) the K split of
+    few-tile prefill grids; returns the previous setting."""
+    return lib().fa_w8a8_set_k_split(max_splits)
+
+
+@contextlib.contextmanager
+def k_split(max_splits):
+    """The K split opted in for the duration of a with-block."""
+    prev = set_k_split(max_splits)
+    try:
+        yield
+    finally:
+        set_k_split(prev)
 
 
 def w8a8_gemm_noalloc(W, w_scale, X, group_size, act_scale=None, smooth_inv=None, out=None):

@@ -157,14 +157,24 @@ int fa_w8a8_gemm_quantized(const int8_t* W, const uint16_t* w_scale, int group_s
                            const int8_t* X_q, const float* X_scale, uint16_t* Y,
                            int M, int N, int K, void* stream);
 
-/* Number of workgroups the linear layer splits K over for this shape (no
- * reference counterpart): 1 means every output is the reference's single
- * group-ordered fp32 chain, bit for bit; n > 1 (prefill grids with few tiles,
- * e.g. 2560 outputs at 512 tokens) means n partial chains over consecutive
- * whole groups, added in split order: the fp16 output then lies within the
- * fp32 reassociation bound (1 fp16 ulp + 2^-20 sum_g |term_g * x_scale_g|)
- * of the reference's, deterministically; the int32 partials are exact either
- * way.  (16-byte aligned operands assumed; fa_w8a8_gemm_noalloc never
+/* Opt-in K split for prefill grids with few tiles (no reference
+ * counterpart).  By default (max_splits <= 1) every output is the
+ * reference's single group-ordered fp32 chain, bit for bit, on every device.
+ * With max_splits >= 3 the linear layer may split K over up to max_splits
+ * (at most 8) workgroups per 128 x 128 tile on grids with fewer tiles than
+ * 256 (2560 outputs at 512 tokens: 80 tiles), each split a partial chain
+ * over consecutive whole groups, the partial sums added in split order.  The
+ * int32 partials stay exact, the result is deterministic and independent of
+ * the device's CU count, but the fp16 output is a reassociation of the
+ * reference's chain: within 1 fp16 ulp + 2^-20 sum_g |term_g * x_scale_g| of
+ * it, which near-zero outputs (|y| << sum_g |term_g|) can take beyond
+ * "1 ulp or rtol 1e-3".  Process-wide; returns the previous setting. */
+int fa_w8a8_set_k_split(int max_splits);
+
+/* Number of workgroups the linear layer splits K over for this shape under
+ * the current fa_w8a8_set_k_split setting: 1 (always, by default) means the
+ * reference's single group-ordered chain, bit for bit; n > 1 as described
+ * there.  (16-byte aligned operands assumed; fa_w8a8_gemm_noalloc never
  * splits.) */
 int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size);
 
@@ -177,10 +187,17 @@ int fa_w8a8_gemm_k_splits(int M, int N, int K, int group_size);
  * wave; 3: the 2..16-token MFMA GEMV) and, when out is non-NULL, fills
  * out[0..9] = kind, grid, block, LDS bytes, 64-byte steps per group, groups
  * per wave, terms-in-LDS flag, in-kernel quantization (0/1/2), epilogue, and
- * 1 if the plan meets the kernels' grid and shape assumptions (every launch
- * checks this and refuses a plan that does not). */
+ * 1 if the plan meets the kernels' grid and shape assumptions.  This reports
+ * the planner's own plan; the entry points drop a plan that fails the check
+ * and take their other path (separate quantizer, prefill kernels), counting
+ * each such drop in fa_debug_gemv_plan_rejects. */
 int fa_debug_gemv_plan(int M, int N, int K, int group_size, int qx, int pro, int epi,
                        int smooth, int* out);
+
+/* Number of decode plans dropped since the library loaded because they
+ * failed the kernels' grid and shape assumptions (0 unless the planner has a
+ * bug; no reference counterpart, for tests). */
+int fa_debug_gemv_plan_rejects(void);
 
 /* Verification hook with no reference counterpart (the reference keeps its
  * int32 partials inside cuBLAS, int8_gemm.cu:476-488): runs exactly the kernel

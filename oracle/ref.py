@@ -190,6 +190,13 @@ def split_chain_tolerance(W, w_scale, group_size, xq, xs, y_ref):
     return ulp + 2.0 ** -20 * np.abs(t).sum(-1)
 
 
+def north_star_tolerance(y_ref):
+    """north_star's bound for fp16 outputs: one fp16 ulp of y_ref or 1e-3
+    relative, whichever is larger.  Returns the bound, float64."""
+    y = np.abs(np.asarray(y_ref, np.float16))
+    return np.maximum(np.spacing(y).astype(np.float64), 1e-3 * y.astype(np.float64))
+
+
 def w8a8_gemm(W, w_scale, group_size, X, act_scale=None, smooth_inv=None):
     W = _c(W, np.int8)
     w_scale = _c(w_scale, np.float16)

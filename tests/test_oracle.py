@@ -250,6 +250,16 @@ def test_split_chain_tolerance(splits):
     err = np.abs(Ys.astype(np.float64) - Y.astype(np.float64))
     assert np.all(err <= bound)
     assert bound.max() < 0.05 * np.abs(Y.astype(np.float64)).max()
+    # north_star's own bound (1 fp16 ulp or rtol 1e-3) holds here too, and
+    # catches what the reassociation bound lets through: a 2-ulp error on
+    # the output nearest zero
+    ns = ref.north_star_tolerance(Y)
+    assert np.all(err <= ns)
+    i = np.unravel_index(np.argmin(np.abs(Y.astype(np.float64)) + (Y == 0)), Y.shape)
+    off = Y.copy()
+    off[i] = np.nextafter(np.nextafter(Y[i], np.float16(np.inf)), np.float16(np.inf))
+    e2 = np.abs(off.astype(np.float64) - Y.astype(np.float64))
+    assert e2[i] > ns[i]
     # plausible mistakes exceed it
     dropped = chain(0, G - 1).astype(np.float16)
     assert np.mean(np.abs(dropped.astype(np.float64) - Y) > bound) > 0.5

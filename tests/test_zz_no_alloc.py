@@ -48,7 +48,8 @@ def run_pair(N, M, K, g, seed, act=None, sm=None):
     ((512, 2560, 4096, 256), (200, 640, 1024, 128)),     # K split in fa_w8a8_gemm, then smaller
 ])
 def test_noalloc_matches_entry_point(first, second):
-    assert _lib.lib().fa_noalloc_scratch_bytes(*first) <= _lib.FA_NOALLOC_SCRATCH_BYTES
+    N, M, K, g = first
+    assert _lib.lib().fa_noalloc_scratch_bytes(M, N, K, g) <= _lib.FA_NOALLOC_SCRATCH_BYTES
     run_pair(*first, seed=1)
     run_pair(*second, seed=2)
 
