@@ -78,11 +78,6 @@ constexpr int kSleep = FA_CHAIN_SLEEP;
 #else
 constexpr int kSleep = 1;
 #endif
-#ifdef FA_CHAIN_AB
-constexpr int kAb = FA_CHAIN_AB;    // measurement builds: 1 = no scale loads (wrong results)
-#else
-constexpr int kAb = 0;
-#endif
 #ifdef FA_CHAIN_PREFETCH
 constexpr bool kPrefetch = true;    // measurement builds: cache prefetch ahead of the ring
 #else
@@ -191,7 +186,7 @@ __global__ __launch_bounds__(NTH, 1) void chain_kernel(const ChainStepDev* __res
                                                       int* __restrict__ flags,
                                                       int spin_limit, ChainLds lay,
                                                       unsigned long long* __restrict__ trace) {
-    constexpr int NOPS = (PF ? 3 : 2) - (kAb == 1 ? 1 : 0);   // global ops per item issue
+    constexpr int NOPS = PF ? 3 : 2;   // global ops per item issue
 #ifdef FA_CHAIN_PFD
     constexpr int PFD = FA_CHAIN_PFD;    // measurement builds: other prefetch distances
 #else
@@ -285,7 +280,7 @@ __global__ __launch_bounds__(NTH, 1) void chain_kernel(const ChainStepDev* __res
         // wave's wait counts exact); those slots are never consumed
         const uint32_t base = ufirst(ring + (uint32_t)slot * kSlot);
         dma16(wp, base);
-        if constexpr (kAb != 1) dma4(sp, base + 1024);
+        dma4(sp, base + 1024);
         if constexpr (PF) {
             const int8_t* pw = steps[0].W;
             const uint16_t* ps;

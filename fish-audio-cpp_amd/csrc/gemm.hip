@@ -301,7 +301,7 @@ __device__ __forceinline__ float ld_coh(const float* p) {
                                  __HIP_MEMORY_SCOPE_AGENT));
 }
 
-template <int BM, int BN, int KS, int kNst, int kOcc, bool kDbg, int kAb = 0>
+template <int BM, int BN, int KS, int kNst, int kOcc, bool kDbg>
 __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ wsT,
     const int8_t* __restrict__ x_q, const float* __restrict__ xsT,
@@ -377,7 +377,6 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
     // Stage `stage`: its A/B tiles plus the scales of the groups that start
     // in stage + 1 (one slot per substep; unused slots fetch a duplicate).
     auto issue = [&](int stage, int u) {
-        if constexpr ((kAb & 8) != 0) return;
         const int st = stage < nstages ? stage : nstages - 1;
         const size_t koff = (size_t)st * KS * 64;
 #pragma unroll
@@ -428,7 +427,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
         for (int u = 0; u < kNst; ++u) {
             const int s = s0 + u;
             if (s >= nstages) break;   // nstages need not be a multiple of kNst
-            if constexpr ((kAb & 8) == 0) wait_vm<kYounger>();
+            wait_vm<kYounger>();
             __syncthreads();
             // groups starting in stage s + 1: their scales came with stage s
 #pragma unroll
@@ -447,28 +446,17 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
                     for (int i = 0; i < RB; ++i) {
                         const int row = wm * 64 + i * 32 + fr;
                         const int c = (q * 4 + kk * 2 + fh) ^ swz<KS>(row);
-                        if constexpr ((kAb & 2) == 0)
-                            a[i] = *reinterpret_cast<const v4i*>(&As[u][(row * CPR + c) * 16]);
-                        else
-                            a[i] = v4i{row, c, s, kk};
+                        a[i] = *reinterpret_cast<const v4i*>(&As[u][(row * CPR + c) * 16]);
                     }
 #pragma unroll
                     for (int j = 0; j < JB; ++j) {
                         const int row = wn * WC + j * 32 + fr;
                         const int c = (q * 4 + kk * 2 + fh) ^ swz<KS>(row);
-                        if constexpr ((kAb & 2) == 0)
-                            bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][(row * CPR + c) * 16]);
-                        else
-                            bb[j] = v4i{c, row, kk, s};
+                        bb[j] = *reinterpret_cast<const v4i*>(&Bs[u][(row * CPR + c) * 16]);
                     }
                     // first MFMA of a K-group starts from zero
                     const bool fresh = kk == 0 && (((s * KS + q) & spg_m1) == 0);
-                    if constexpr ((kAb & 1) != 0) {
-#pragma unroll
-                        for (int i = 0; i < RB; ++i)
-#pragma unroll
-                            for (int j = 0; j < JB; ++j) P[i][j][0] ^= a[i].x ^ bb[j].y;
-                    } else if (fresh) {
+                    if (fresh) {
 #pragma unroll
                         for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -486,7 +474,7 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
                 }
                 const int tcur = s * KS + q;
                 // a group ends with its last substep, or (K % g != 0) with K
-                if ((kAb & 4) == 0 && (((tcur + 1) & spg_m1) == 0 || tcur + 1 == nsub)) {
+                if (((tcur + 1) & spg_m1) == 0 || tcur + 1 == nsub) {
                     const int gi = tcur >> lg_spg;
                     const int sl = gi & 3;
 #pragma unroll
@@ -512,14 +500,6 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
         }
     }
     wait_vm<0>();   // no direct-to-LDS write may outlive the workgroup
-    if constexpr ((kAb & 4) != 0) {
-#pragma unroll
-        for (int i = 0; i < RB; ++i)
-#pragma unroll
-            for (int j = 0; j < JB; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] += (float)P[i][j][e];
-    }
 
     // fp16 out: each lane holds 4 consecutive rows of one token per (i, j, e/4)
     const bool vec = (M & 3) == 0;
@@ -575,17 +555,12 @@ __global__ __launch_bounds__(BM * 2, kOcc) void gemm_pipe_kernel(
 // A group's epilogue runs at the first K step of the next group, each block's
 // scaling next to that block's first MFMA of the new group, so the VALU work
 // of one block overlaps the matrix work of the others.
-// kAb (measurement builds only; 0 in the library): 1 drops the MFMAs, 2 the
-// fragment reads, 4 the epilogue (one add per block and group remains, so the
-// MFMA chains stay live), 8 the global->LDS loads (the tiles are filled once
-// instead, so the fragment reads stay live).
-//
 // DIRECT: the scales come straight from the reference layouts instead of the
 // group-major tables: weight lane r fetches the aligned fp16 pair that holds
 // w_scale[row, g] (4 bytes; the epilogue picks the half), token lanes fetch
 // x_scale[tok, g].  One gather instruction per wave and group, cheap while a
 // row's G scales are few (g >= 128 here), and no table launch.
-template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, int kAb = 0, bool kSched = true,
+template <int BM, int BN, int NST, int LGS, int kOcc, bool kDbg, bool kSched = true,
           bool DIRECT = false, bool SPLIT = false>
 __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ wsT,
@@ -609,14 +584,6 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     __shared__ __align__(16) int8_t At[NST][BN * 128];   // tokens, 128 B per row and stage
     __shared__ __align__(16) int8_t Bt[NST][BM * 128];   // weight rows
     __shared__ __align__(16) float sc[NSS][BM + BN];     // [0, BM) weight scales, then tokens
-    if constexpr ((kAb & 8) != 0) {
-        // no tile loads: give the fragment reads defined (varying) contents
-        for (int i = threadIdx.x; i < NST * BN * 32; i += blockDim.x)
-            reinterpret_cast<uint32_t*>(At)[i] = (uint32_t)i * 2654435761u;
-        for (int i = threadIdx.x; i < NST * BM * 32; i += blockDim.x)
-            reinterpret_cast<uint32_t*>(Bt)[i] = (uint32_t)i * 40503u + 7u;
-        __syncthreads();
-    }
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -694,7 +661,6 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     // re-fetches one of its groups into the same slot).  Stages past the end
     // re-fetch the last stage so every wave's load count stays uniform.
     auto issue = [&](int st, int u) {
-        if constexpr ((kAb & 8) != 0) return;
         const int sc_st = st0 + min(max(st, 0), nst - 1);   // absolute stage
         const size_t koff = (size_t)sc_st * 128;
 #pragma unroll
@@ -777,11 +743,6 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
     };
     // scale group gi's finished accumulators of block (i, j) into acc
     auto epi = [&](int gi, const Scales& sv, int i, int j) {
-        if constexpr ((kAb & 4) != 0) {
-            // one operation per block: keeps every MFMA chain live
-            acc[i][j][0] += __int_as_float(P[i][j][0]);
-            return;
-        }
         const float ws = sv.ws[j];
         const float nws = sv.nws[j];
 #pragma unroll
@@ -840,19 +801,13 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
                     // these per slot in registers across the loop)
                     uint32_t off = alane[i] ^ (uint32_t)((q * 4 + kk * 2) * 16);
                     asm volatile("" : "+v"(off));
-                    if constexpr ((kAb & 2) == 0)
-                        a[i] = *reinterpret_cast<const v4i*>(&At[slot][off]);
-                    else
-                        a[i] = v4i{(int)off, q, s, 0x01020304};
+                    a[i] = *reinterpret_cast<const v4i*>(&At[slot][off]);
                 }
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     uint32_t off = blane[j] ^ (uint32_t)((q * 4 + kk * 2) * 16);
                     asm volatile("" : "+v"(off));
-                    if constexpr ((kAb & 2) == 0)
-                        bb[j] = *reinterpret_cast<const v4i*>(&Bt[slot][off]);
-                    else
-                        bb[j] = v4i{kk, (int)off, 0x05060708, s};
+                    bb[j] = *reinterpret_cast<const v4i*>(&Bt[slot][off]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (kk == 0 && fresh) {
@@ -872,11 +827,8 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
                             // then restart its accumulators; the MFMA of one
                             // block runs under the scaling of the next
                             epi(gprev, sv, i, j);
-                            if constexpr ((kAb & 1) == 0)
-                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], magic,
-                                                                                0, 0, 0);
-                            else
-                                P[i][j] = magic ^ a[i].x ^ bb[j].y;
+                            P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], magic, 0,
+                                                                            0, 0);
                             if constexpr (!kDbg && kSched) {
                                 __builtin_amdgcn_sched_group_barrier(0x100, 5, 0);
                                 __builtin_amdgcn_sched_group_barrier(0x002, 33, 0);
@@ -890,11 +842,8 @@ __global__ __launch_bounds__(BM * BN / 64, kOcc) void gemm_tile_kernel(
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
                         for (int j = 0; j < 2; ++j) {
-                            if constexpr ((kAb & 1) == 0)
-                                P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                                    a[i], bb[j], P[i][j], 0, 0, 0);
-                            else
-                                P[i][j][0] ^= a[i].x ^ bb[j].y;
+                            P[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], P[i][j],
+                                                                            0, 0, 0);
                         }
                 }
             }
@@ -1215,11 +1164,11 @@ hipError_t launch_gemm_tile(const int8_t* W, const uint16_t* w_scale, const int8
     const dim3 grid((unsigned)(tm * tn), (unsigned)nsplit);
 #define FA_TILE_S(BMV, NSTV, OCCV, LGS, DIR, SPL)                                                \
     if (dbg_partials)                                                                            \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true, 0, true, DIR, SPL>), \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, true, true, DIR, SPL>), \
                            grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
                            tm, tn, w_scale, x_scale, nsplit, part, tile_cnt);                    \
     else                                                                                         \
-        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false, 0, true, DIR, SPL>), \
+        hipLaunchKernelGGL((gemm_tile_kernel<BMV, 128, NSTV, LGS, OCCV, false, true, DIR, SPL>), \
                            grid, dim3(BMV * 2), 0, stream, W, wsT, x_q, xsT, Y, dbg, M, N, K, G, \
                            tm, tn, w_scale, x_scale, nsplit, part, tile_cnt);
 // (K splits run only on 128 x 128 tiles, the shape of the few-tile grids)

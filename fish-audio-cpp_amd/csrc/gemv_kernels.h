@@ -341,7 +341,7 @@ __device__ __forceinline__ void qx_stage(QxIn<XV, PRO>& in, const uint16_t* __re
 // both chains, rounds each to fp16 (the reference's two GEMMs output fp16)
 // and stores act[i] = fp16(fp16(silu(gate)) * up) (silu_forward then
 // mul_forward, ffn_activations.cu:12-17, 35-39) into Y [M / 2].
-template <int R, int KD, int LG, bool QX, int XV, int NWV = kDotWaves, int kAb = 0, int PRO = 0,
+template <int R, int KD, int LG, bool QX, int XV, int NWV = kDotWaves, int PRO = 0,
           int EPI = 0>
 __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
@@ -422,10 +422,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         } else {
             const int8_t* wrow = row < M ? W + (size_t)row * K : wlast;
             const v4i wa = ld16(wrow + kk);
-            if constexpr ((kAb & 2) == 0)
-                sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
-            else
-                sc[slot] = (uint16_t)kk;
+            sc[slot] = w_scale[G == 1 ? (size_t)rowc : (size_t)rowc * G + (kk >> lg_g)];
             a[slot] = wa;
         }
         if (++l_pass == passes) {
@@ -437,8 +434,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
     for (int s = 0; s < KD; ++s) load(s);
 
     // ---- stage activations into LDS
-    if constexpr ((kAb & 1) != 0) {
-    } else if constexpr (!QX) {
+    if constexpr (!QX) {
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
             const int k = (tid + i * NT) * 16;
@@ -457,7 +453,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
             qx_stage<XV, NT, PRO>(qin, X, act_scale, smooth_inv, K, lg_g, G, pro, tid,
                                   blockIdx.x == 0, xq_s, xs_s, h_s, red_s);
     }
-    if constexpr ((kAb & 1) == 0) __syncthreads();
+    __syncthreads();
 
     // ---- consume
     int c_blk = blockIdx.x, c_pass = 0;     // consume cursor (uniform)
@@ -468,7 +464,7 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
         const int kbase = c_pass * PB;                 // row offset of this pass (uniform)
         const int k = kbase + lane_k;
         const int8_t* xqr = (EPI == 2 && rsub == 1) ? xq3_s : xq_s;   // EPI 2: the row's codes
-        v4i b = (kAb & 1) ? a[slot] : *reinterpret_cast<const v4i*>(xqr + (k < K ? k : 0));
+        v4i b = *reinterpret_cast<const v4i*>(xqr + (k < K ? k : 0));
         if (k >= K) b = zero;
         int p = __builtin_amdgcn_sdot4(a[slot].x, b.x, 0, false);
         p = __builtin_amdgcn_sdot4(a[slot].y, b.y, p, false);
@@ -481,39 +477,35 @@ __global__ __launch_bounds__(NWV * 64) void gemv_dot_kernel(
             if (k < K && (li & (LG - 1)) == 0 && row < M && dbg.in(row, 0))
                 dbg.at(row, 0, k >> lg_g, G) = p;
         }
-        if constexpr ((kAb & 4) != 0) {
-            acc[0] += term;
-        } else {
-            // group order within the pass: slot j of every row; the pass's
-            // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
-            // (EPI 2: row slot 1 takes the up weight's token scales)
-            constexpr int NXS = EPI == 2 ? 2 : 1;
-            float xsv[NXS][GPP];
+        // group order within the pass: slot j of every row; the pass's
+        // GPP scales come in one LDS read (kbase / g is a multiple of GPP)
+        // (EPI 2: row slot 1 takes the up weight's token scales)
+        constexpr int NXS = EPI == 2 ? 2 : 1;
+        float xsv[NXS][GPP];
 #pragma unroll
-            for (int q = 0; q < NXS; ++q) {
-                const float* xp = (q ? xs3_s : xs_s) + (kbase >> lg_g);
-                if constexpr (GPP == 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(xp);
-                    xsv[q][0] = v.x; xsv[q][1] = v.y; xsv[q][2] = v.z; xsv[q][3] = v.w;
-                } else if constexpr (GPP == 2) {
-                    const float2 v = *reinterpret_cast<const float2*>(xp);
-                    xsv[q][0] = v.x; xsv[q][1] = v.y;
-                } else {
+        for (int q = 0; q < NXS; ++q) {
+            const float* xp = (q ? xs3_s : xs_s) + (kbase >> lg_g);
+            if constexpr (GPP == 4) {
+                const float4 v = *reinterpret_cast<const float4*>(xp);
+                xsv[q][0] = v.x; xsv[q][1] = v.y; xsv[q][2] = v.z; xsv[q][3] = v.w;
+            } else if constexpr (GPP == 2) {
+                const float2 v = *reinterpret_cast<const float2*>(xp);
+                xsv[q][0] = v.x; xsv[q][1] = v.y;
+            } else {
 #pragma unroll
-                    for (int j = 0; j < GPP; ++j) xsv[q][j] = xp[j];
-                }
+                for (int j = 0; j < GPP; ++j) xsv[q][j] = xp[j];
             }
+        }
 #pragma unroll
-            for (int j = 0; j < GPP; ++j) {
-                const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
-                if (kg < K) {
+        for (int j = 0; j < GPP; ++j) {
+            const int kg = kbase + j * LG * 16;        // first byte of slot j (uniform)
+            if (kg < K) {
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const float tj = __builtin_bit_cast(
-                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
-                                                             r * RL + j * LG));
-                        acc[r] = __builtin_fmaf(tj, xsv[NXS == 2 ? r : 0][j], acc[r]);
-                    }
+                for (int r = 0; r < R; ++r) {
+                    const float tj = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term),
+                                                         r * RL + j * LG));
+                    acc[r] = __builtin_fmaf(tj, xsv[NXS == 2 ? r : 0][j], acc[r]);
                 }
             }
         }
@@ -565,7 +557,7 @@ __device__ __forceinline__ uint16_t swiglu_h(uint16_t gate, uint16_t up) {
 
 // QX: 0 = staged int8 codes (x_q, x_scale), 1 = quantize X in-kernel,
 // 2 = the same times smooth_inv.  EPI 1: SwiGLU pairs (M even).
-template <int SPG, int MAXG, bool LC, bool kDbg, int kAb = 0, int kKD = 12, int QX = 0,
+template <int SPG, int MAXG, bool LC, bool kDbg, int kKD = 12, int QX = 0,
           int EPI = 0>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     const int8_t* __restrict__ W, const uint16_t* __restrict__ w_scale,
@@ -645,9 +637,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
     auto load = [&](int slot, int step) {
         const size_t off = (size_t)(step < nvalid ? step : 0) * 64;
         a[slot] = ld16(wp + off);
-        if constexpr (BH) {
-        } else if constexpr ((kAb & 1) == 0) b[slot] = ld16(xp + off);
-        else b[slot] = a[slot];
+        if constexpr (!BH) b[slot] = ld16(xp + off);
     };
     // Scales of the tile's 16 rows and of the tokens, all groups: at most 5
     // per thread (the plan keeps G <= 20 * NW).  Their loads go out before
@@ -724,7 +714,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(
 #pragma unroll
     for (int q = 0; q < kSt; ++q) {
         const int i = threadIdx.x + q * blockDim.x;
-        if ((kAb & 4) == 0 && i < kTile * G) {
+        if (i < kTile * G) {
             ws_s[i] = h2f(wsr[q]);
             if constexpr (!QX) xs_s[i] = xsr[q];
         }
@@ -878,10 +868,10 @@ DotFn dot_swiglu(int pro, int K, int kd, int lgl, bool sep = false);  // gemv_do
 template <int R, int KD, bool QX, int XV, int NWV, int PRO, int EPI>
 DotFn dot_for_lg(int lg) {
     switch (lg) {
-        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, NWV, 0, PRO, EPI>;     // g64
-        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, NWV, 0, PRO, EPI>;     // g128
-        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, NWV, 0, PRO, EPI>;    // g256
-        default: return gemv_dot_kernel<R, KD, 32, QX, XV, NWV, 0, PRO, EPI>;   // g512
+        case 2: return gemv_dot_kernel<R, KD, 4, QX, XV, NWV, PRO, EPI>;     // g64
+        case 3: return gemv_dot_kernel<R, KD, 8, QX, XV, NWV, PRO, EPI>;     // g128
+        case 4: return gemv_dot_kernel<R, KD, 16, QX, XV, NWV, PRO, EPI>;    // g256
+        default: return gemv_dot_kernel<R, KD, 32, QX, XV, NWV, PRO, EPI>;   // g512
     }
 }
 

@@ -11,7 +11,7 @@ template <int SPG, int MAXG, bool LC, int QX, int EPI>
 MfmaFn<false> inst() {
     constexpr int lim = QX == 2 ? kMfmaQxStepsSmooth : kMfmaQxSteps;
     if constexpr (QX != 0 && SPG * MAXG > lim) return nullptr;
-    else return gemv_mfma_kernel<SPG, MAXG, LC, false, 0, 12, QX, EPI>;
+    else return gemv_mfma_kernel<SPG, MAXG, LC, false, 12, QX, EPI>;
 }
 
 template <int SPG, bool LC, int QX, int EPI>

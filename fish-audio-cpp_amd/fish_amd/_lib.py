@@ -4,11 +4,13 @@ Loading fails loudly: there is no CPU or PyTorch fallback for any entry point.
 """
 import ctypes
 import os
+import sys
 
 from .build import LIB_PATH as _BUILT_LIB
 
-# FISH_W8A8_LIB selects another build of the library (e.g. a measurement
-# build); by default the in-tree build is loaded.
+# FISH_W8A8_LIB selects another build of the library; by default the in-tree
+# build is loaded.  A redirected load is announced on stderr with its path,
+# so no test or benchmark output can silently come from another build.
 LIB_PATH = os.environ.get("FISH_W8A8_LIB") or _BUILT_LIB
 
 FA_OK = 0
@@ -137,6 +139,9 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 "libfish_w8a8.so is not built (%s); run __graft_entry__.build()" % LIB_PATH)
+        if LIB_PATH != _BUILT_LIB:
+            sys.stderr.write("fish_w8a8: FISH_W8A8_LIB is set; loading %s instead of %s\n"
+                             % (os.path.abspath(LIB_PATH), _BUILT_LIB))
         l = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(l, name)

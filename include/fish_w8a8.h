@@ -59,8 +59,11 @@ int fa_w8a8_gemm(const int8_t* W, const uint16_t* w_scale, int group_size,
 
 /* No counterpart in the reference: fa_w8a8_gemm for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
- * fa_w8a8_gemm, bit for bit; it never calls hipMalloc / hipFree.  Its scratch
+ * harnesses that forbid hipMalloc).  Same arguments as fa_w8a8_gemm, and the
+ * reference's results bit for bit, as fa_w8a8_gemm gives them by default;
+ * the kernel choice can differ (at 2..16 tokens it always quantizes in a
+ * separate launch, and it never splits K even when fa_w8a8_set_k_split has
+ * opted fa_w8a8_gemm in).  It never calls hipMalloc / hipFree.  Its scratch
  * (x_q, x_scale and the prefill scale tables, fa_noalloc_scratch_bytes()
  * bytes) lives in one statically sized device array of
  * FA_NOALLOC_SCRATCH_BYTES per device, held until the process ends; shapes
@@ -345,9 +348,20 @@ typedef struct fa_chain fa_chain;
  * steps and uploads the step table (allocates device memory: call once,
  * outside a capture).  All steps share group_size (64, 128 or 256). */
 int fa_chain_create(const fa_chain_step* steps, int n_steps, int group_size, fa_chain** out);
-/* Run the chain on `stream` (a counter reset and one cooperative launch;
- * no allocation, no host sync).
- * Runs on one stream at a time: overlapping runs of one chain race. */
+/* Run the chain on `stream`: a small kernel that zeroes the step counters,
+ * then one ordinary launch of one workgroup per CU (576 threads, one per CU
+ * by its LDS use).  No allocation, no host sync.
+ * The launch is not cooperative: the steps order themselves through device
+ * counters, which assumes every workgroup of the grid is resident at once.
+ * That holds on an otherwise idle device; kernels running concurrently on
+ * other streams can keep workgroups from starting.  Every wait is bounded
+ * (fa_chain_set_spin_limit), so the kernel always finishes; when a wait gave
+ * up, fa_chain_status reports FA_ERR_HIP and the outputs of that run are
+ * incomplete (run it again, or take the per-linear entry points).
+ * Runs on one stream at a time: overlapping runs of one chain race.
+ * Experimental: measured slower than the four fused launches per layer
+ * (fa_w8a8_gemm_rms / _swiglu / fa_w8a8_gemm) and limited to dynamic
+ * quantization, so the engine path is those entry points. */
 int fa_chain_run(fa_chain* chain, void* stream);
 /* Wait for `stream`, then report whether the last run finished: FA_ERR_HIP
  * when a step's wait for its predecessor gave up (spin limit reached), in
