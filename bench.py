@@ -44,7 +44,7 @@ def cpu_baseline(stack, torch, budget_s):
     from oracle import ref
     from fish_amd.synth import LAYER_SHAPES
     march = ref.use_baseline_build()
-    model = ref.host_cpu()[0]
+    model = ref.host_cpu_id()
     lay = stack.layers[0]
     host = {}
     nbytes = 0
@@ -74,6 +74,45 @@ def cpu_baseline(stack, torch, budget_s):
                       "%d reps, median %.2f ms" % (len(times), med * 1e3)}
 
 
+def cpu_baseline_prefill(budget_s):
+    """configs[3] on the host: the C oracle (the reference's W8A8 math:
+    per-token, per-group activation quantization, int32 group partials,
+    the group-ordered fp32 chain, fp16 out; OpenMP over output rows) for
+    one layer's four linears at 512 and 2048 tokens, g256, the whole layer
+    (no row sampling), on the same synthetic distributions as the GPU
+    figures.  Reports int8 TOP/s (2*M*N*K per linear) for the median
+    repetition; at least one repetition, more while budget_s lasts."""
+    from oracle import ref
+    from fish_amd import synth
+    from fish_amd.synth import LAYER_SHAPES
+    march = ref.use_baseline_build()
+    g = 256
+    wts = {name: ref.quantize_weights(synth.weights_f16(N, K, seed=31 + i), g)
+           for i, (name, (K, N)) in enumerate(LAYER_SHAPES.items())}
+    res = {"unit": "TOP/s", "cores": ref.num_threads(), "kind": "port",
+           "cpu_model": ref.host_cpu_id(), "build": "gcc -O3 -fopenmp -march=%s" % march}
+    for M in (512, 2048):
+        xs = {name: synth.activations_f16(M, K, seed=M + i)
+              for i, (name, (K, N)) in enumerate(LAYER_SHAPES.items())}
+        ops_layer = sum(2.0 * M * N * K for K, N in LAYER_SHAPES.values())
+        times = []
+        t_end = time.perf_counter() + budget_s / 2
+        while not times or (time.perf_counter() < t_end and len(times) < 5):
+            t0 = time.perf_counter()
+            for name, (q, sc) in wts.items():
+                ref.w8a8_gemm(q, sc, g, xs[name])
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        res["m%d_g256_layer_TOPS" % M] = round(ops_layer / med / 1e12, 4)
+        res["m%d_g256_layer_ms" % M] = round(med * 1e3, 1)
+        res["m%d_reps" % M] = len(times)
+    res["value"] = res["m2048_g256_layer_TOPS"]
+    res["sample"] = ("one layer's 4 linears (qkv/o/gate_up/down), full size, at 512 and "
+                     "2048 tokens, g256, fa_w8a8_gemm semantics incl. activation "
+                     "quantization; value = the 2048-token layer")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +120,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-prefill-budget", type=float, default=20.0)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate_up GEMV event timing (for rocprofv3 runs)")
@@ -88,7 +128,7 @@ def main():
                     help="only the configs[4] four-launch stack, graph-replayed 13 times "
                          "(for rocprofv3 runs)")
     ap.add_argument("--chain-only", action="store_true",
-                    help="only the configs[4] decode chain, 20 runs (for rocprofv3 runs)")
+                    help="only the experimental configs[4] decode chain, 20 runs (for rocprofv3 runs)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the T=2048 prefill attention side (for rocprofv3 runs)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -184,6 +224,7 @@ def main():
     del st
     torch.cuda.empty_cache()
     roofline_pf = roofline_prefill(torch, ops)
+    cpu_pf = cpu_baseline_prefill(args.cpu_prefill_budget)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -198,6 +239,7 @@ def main():
         "roofline": roofline,
         "roofline_prefill": roofline_pf,
         "cpu_baseline": cpu,
+        "cpu_baseline_prefill": cpu_pf,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
@@ -316,23 +358,6 @@ def run_secondary(torch, ops, st, args):
     t = (time.perf_counter() - t0) / reps
     out["cfg4_stack_g256_m1"] = {"step_ms": round(t * 1e3, 4),
                                  "GB/s": round(st.stack_bytes() / t / 1e9, 1)}
-    # the same stack as one device-ordered launch (fa_chain; eager: one
-    # cooperative launch plus a counter reset and the last residual add)
-    st.h.copy_(st.h0)
-    st.build_chain()
-    for _ in range(2):
-        st.run_chain(check=False)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        st.run_chain(check=False)
-    torch.cuda.synchronize()
-    t = (time.perf_counter() - t0) / reps
-    out["cfg4_chain_g256_m1"] = {"step_ms": round(t * 1e3, 4),
-                                 "GB/s": round(st.stack_bytes() / t / 1e9, 1),
-                                 "complete": st.chain.status() == 0}
-    st.chain.close()
-    st.chain = None
     # configs[4] with the calibrated (AWQ) layout a real dual_ar.bin carries:
     # wqkv / w1 / w3 with their own smooth_inv, w1 and w3 separate weights
     # (four launches per layer: w1 and w3 in one fa_w8a8_gemm_swiglu_sep)
@@ -457,6 +482,8 @@ def run_secondary(torch, ops, st, args):
 
     # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
     out.update(prefill_tops(torch, ops, [(256, 512), (256, 2048), (64, 2048)]))
+    out.update(prefill_k_split(torch, ops))
+    out.update(tp_shard_lines(torch, ops))
     out.update(vendor_int8_gemm(torch))
     out.update(attention_side(torch, ops))
     return out
@@ -527,6 +554,73 @@ def vendor_int8_gemm(torch):
         out["vendor_int8_mm_m2048_%s_TOPS" % name] = round(o / (us * 1e-6) / 1e12, 1)
     if tot_us > 0:
         out["vendor_int8_mm_m2048_layer_TOPS"] = round(tot_ops / (tot_us * 1e-6) / 1e12, 1)
+    return out
+
+
+# One GPU's share of each linear under 8-way tensor parallelism: qkv and
+# gate_up split their output rows, o and down their K (on group boundaries
+# where g divides the share; down's 1216 leaves a short last group at g256).
+TP8_SHAPES = {"qkv": (2560, 768), "o": (512, 2560), "gate_up": (2560, 2432),
+              "down": (1216, 2560)}
+
+
+def tp_shard_lines(torch, ops, layers=36, g=256):
+    """The TP=8 shard shapes on one GPU: decode (1 token, fa_w8a8_gemm with
+    in-kernel quantization, `layers` distinct weight copies per graph so
+    every launch reads from HBM) in GB/s of algorithmic bytes, and prefill
+    (2048 tokens, fa_w8a8_gemm_quantized) in int8 TOP/s."""
+    out = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(21)
+    for name, (K, N) in TP8_SHAPES.items():
+        G = (K + g - 1) // g
+        ws = []
+        for _ in range(layers):
+            w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+            ws.append(ops.quantize_weights_groupwise(w, g))
+        x = torch.randn((1, K), generator=gen, device="cuda").half()
+        y = torch.empty((1, N), device="cuda", dtype=torch.float16)
+        us = graph_us_per_call(torch, [(lambda W=W, S=S: ops.w8a8_gemm(W, S, x, g, out=y))
+                                       for W, S in ws])
+        b = N * K + 2 * N * G + 2 * (K + N)
+        out["tp8_gemv_m1_g256_%s_us" % name] = round(us, 2)
+        out["tp8_gemv_m1_g256_%s_GBs" % name] = round(b / (us * 1e-6) / 1e9, 1)
+        M = 2048
+        xp = torch.randn((M, K), generator=gen, device="cuda").half()
+        xq, xs = ops.quantize_activations(xp, g)
+        yp = torch.empty((M, N), device="cuda", dtype=torch.float16)
+        W, S = ws[0]
+        us = graph_us_per_call(torch, [lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=yp)]
+                               * 8, reps=5)
+        out["tp8_gemm_m2048_g256_%s_us" % name] = round(us, 2)
+        out["tp8_gemm_m2048_g256_%s_TOPS" % name] = round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1)
+        del ws, xp, xq, xs, yp
+        torch.cuda.empty_cache()
+    return out
+
+
+def prefill_k_split(torch, ops):
+    """o and down at 512 tokens, g256, with the opt-in K split
+    (fa_w8a8_set_k_split(8): partial chains added in split order, within
+    1 ulp / rtol 1e-3 of the reference's chain rather than bit-exact) --
+    beside the default exact figures of prefill_tops."""
+    from fish_amd.synth import LAYER_SHAPES
+    out = {}
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    M, g = 512, 256
+    for name in ("o", "down"):
+        K, N = LAYER_SHAPES[name]
+        w = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+        W, S = ops.quantize_weights_groupwise(w, g)
+        x = torch.randn((M, K), generator=gen, device="cuda").half()
+        xq, xs = ops.quantize_activations(x, g)
+        y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+        with ops.k_split(8):
+            us = graph_us_per_call(torch, [lambda: ops.w8a8_gemm_quantized(W, S, g, xq, xs, out=y)]
+                                   * 8, reps=5)
+            out["cfg3_gemm_m512_g256_%s_ksplit%d_us" % (name, ops.k_splits(N, M, K, g))] = \
+                round(us, 2)
     return out
 
 

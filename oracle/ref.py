@@ -63,6 +63,29 @@ def host_cpu():
     return model, v4
 
 
+def host_cpu_id():
+    """'<model name> (family F, model M, stepping S), <logical CPUs> logical
+    CPUs' from /proc/cpuinfo: enough to tell two hosts whose model names
+    read the same apart."""
+    info = {}
+    n = 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" not in line:
+                    continue
+                k, v = (t.strip() for t in line.split(":", 1))
+                if k == "processor":
+                    n += 1
+                elif k in ("model name", "cpu family", "model", "stepping") and k not in info:
+                    info[k] = v
+    except OSError:
+        pass
+    return "%s (family %s, model %s, stepping %s), %d logical CPUs" % (
+        info.get("model name", "unknown"), info.get("cpu family", "?"), info.get("model", "?"),
+        info.get("stepping", "?"), n)
+
+
 def use_baseline_build():
     """For the CPU-baseline timing only: load the x86-64-v4 build when this
     host has AVX-512 (call before any other oracle function).  Returns the

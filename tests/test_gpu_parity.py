@@ -681,3 +681,32 @@ def test_decode_stack_bitexact(g, T):
                                        np.ascontiguousarray(y[:, 1::2]), g)
         h = ref.residual_add(h, lin("down", xq, xs))
     assert same(host(st.h), h)
+
+
+# One GPU's share under 8-way tensor parallelism: qkv and gate_up split
+# their output rows, o and down their K (down's 1216 leaves a short last
+# group at g256; o's 512 is two groups).
+TP8 = {"qkv": (2560, 768), "o": (512, 2560), "gate_up": (2560, 2432), "down": (1216, 2560)}
+
+
+@pytest.mark.parametrize("name", list(TP8))
+@pytest.mark.parametrize("N,g", [(1, 256), (8, 64), (8, 256), (16, 256), (512, 256),
+                                 (2048, 256)])
+def test_tp8_shard_shapes(name, N, g):
+    """TP=8 shard shapes through fa_w8a8_gemm_partials (every int32 group
+    partial up to 16 tokens, a 64 x 64 window beyond) and fa_w8a8_gemm:
+    bit-exact against the oracle."""
+    K, Nout = TP8[name]
+    if N <= 16:
+        check_linear(N, Nout, K, g, seed=50 + N)
+        return
+    q, s = make_linear(Nout, K, g, seed=60)
+    x = synth.activations_f16(N, K, seed=61)
+    rq, rs = ref.quantize_activations(x, g)
+    r0, t0 = Nout // 2 - 32, N // 3
+    Y, P = ops.w8a8_gemm_partials(dev(q), dev(s), g, dev(rq), dev(rs), row0=r0, rows=64,
+                                  tok0=t0, toks=64)
+    assert same(host(P), ref.group_partials(q[r0:r0 + 64], rq[t0:t0 + 64], g))
+    assert same(host(Y), ref.gemm_quantized(q, s, g, rq, rs))
+    Y2 = ops.w8a8_gemm(dev(q), dev(s), dev(x), g)
+    assert same(host(Y2), host(Y))

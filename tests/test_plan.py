@@ -89,3 +89,24 @@ def test_plans_refused_where_the_kernels_do_not_go():
     assert plan(100, 8, 512, 64, epi=2)["kind"] == 0    # separate w1 / w3: one token only
     assert plan(100, 2, 512, 64, qx=1, pro=2)["kind"] == 0   # fused prologue: one token only
     assert plan(100, 1, 40000, 64, qx=1)["kind"] == 0   # K beyond the one-token kernels
+
+
+TP8 = {"qkv": (2560, 768), "o": (512, 2560), "gate_up": (2560, 2432), "down": (1216, 2560)}
+
+
+@pytest.mark.parametrize("name", list(TP8))
+@pytest.mark.parametrize("g", [256, 64])
+def test_tp8_shard_shapes_plan(name, g):
+    """One GPU's share under 8-way tensor parallelism (o and down split K:
+    2 groups of 256, or 4.75 -- a short last group for down at g256): the
+    decode paths plan them and every plan meets the kernel assumptions."""
+    K, M = TP8[name]
+    for N in (1, 2, 8, 16):
+        for qx, pro, epi, sm in [(0, 0, 0, 0), (1, 0, 0, 0), (1, 0, 0, 1), (1, 2, 0, 0),
+                                 (1, 1, 0, 0), (1, 0, 1, 0), (1, 2, 1, 0)]:
+            d = plan(M, N, K, g, qx, pro, epi, sm)
+            if d["kind"]:
+                assert d["valid"] == 1, (name, g, N, qx, pro, epi, sm, d)
+    assert plan(M, 1, K, g, qx=1)["kind"] in (1, 2)
+    assert plan(M, 8, K, g)["kind"] == 3
+
