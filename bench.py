@@ -132,7 +132,9 @@ def main():
     ap.add_argument("--attn-only", action="store_true",
                     help="only the T=2048 prefill attention side (for rocprofv3 runs)")
     ap.add_argument("--prefill-only", action="store_true",
-                    help="only the configs[3] M=2048 g256 prefill GEMMs (for rocprofv3 runs)")
+                    help="only the configs[3] g256 prefill GEMMs at --prefill-tokens "
+                         "(for rocprofv3 runs)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -149,7 +151,7 @@ def main():
         print(json.dumps(attention_side(torch, ops)), flush=True)
         return
     if args.prefill_only:
-        print(json.dumps(prefill_tops(torch, ops, [(256, 2048)])), flush=True)
+        print(json.dumps(prefill_tops(torch, ops, [(256, args.prefill_tokens)])), flush=True)
         return
     log("building 36-layer g256 weight set ...")
     st = DecodeStack(n_layers=args.layers, g=256, tokens=1, seed=0)
