@@ -226,7 +226,10 @@ def main():
     del st
     torch.cuda.empty_cache()
     roofline_pf = roofline_prefill(torch, ops)
-    cpu_pf = cpu_baseline_prefill(args.cpu_prefill_budget)
+    try:
+        cpu_pf = cpu_baseline_prefill(args.cpu_prefill_budget)
+    except Exception as e:   # noqa: BLE001 -- reported in the JSON line
+        cpu_pf = {"error": "%s: %s" % (type(e).__name__, str(e)[:160])}
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -484,8 +487,13 @@ def run_secondary(torch, ops, st, args):
 
     # prefill, M=512 / 2048, g256 (and g64 at 2048), int8 TOPS
     out.update(prefill_tops(torch, ops, [(256, 512), (256, 2048), (64, 2048)]))
-    out.update(prefill_k_split(torch, ops))
-    out.update(tp_shard_lines(torch, ops))
+    # (a failure in one of these lines is recorded, not fatal to the bench line)
+    for name, fn in (("prefill_k_split", prefill_k_split), ("tp8_shards", tp_shard_lines)):
+        try:
+            out.update(fn(torch, ops))
+        except Exception as e:   # noqa: BLE001 -- reported in the JSON line
+            out[name + "_error"] = "%s: %s" % (type(e).__name__, str(e)[:160])
+            torch.cuda.synchronize()
     out.update(vendor_int8_gemm(torch))
     out.update(attention_side(torch, ops))
     return out
